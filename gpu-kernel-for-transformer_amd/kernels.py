@@ -1,0 +1,209 @@
+"""Tensor-level wrappers over the C-ABI, mirroring the reference's kernel API.
+
+`layer_norm` and `fused_residual_layer_norm` keep the names, argument meaning
+and error behaviour of triton_fused_norm.py:140-215 (ValueError for device or
+shape mismatches, RuntimeError when the kernels are unavailable).  `linear`,
+`ffn_gelu` and `causal_attention` replace F.linear (torch_transformer_benchmark.py:685,
+:741), triton_ffn_gelu (triton_fused_ffn.py:224-261) and the SDPA dispatch
+(torch_transformer_benchmark.py:767-809).  The GEMM wrappers take weights in
+nn.Linear's own [out, in] layout: both MFMA operands are then K-contiguous,
+so the reference's cached [in, out] transposes have no counterpart here.
+
+All wrappers allocate their outputs with torch (the caller owns them), enqueue
+on torch's current stream, and never synchronise: they are capture-safe.
+"""
+
+from __future__ import annotations
+
+from functools import lru_cache
+from typing import Optional, Tuple
+
+import torch
+
+from . import _capi
+from ._capi import XB_EPI_BIAS, XB_EPI_BIAS_GELU, XB_F16, XB_F32, check, lib, stream_handle
+
+_DTYPE_CODES = {torch.float32: XB_F32, torch.float16: XB_F16}
+
+
+@lru_cache(maxsize=None)
+def _device_is_gfx950(index: int) -> bool:
+    return _capi.gfx_arch(torch.device("cuda", index)) == "gfx950"
+
+
+def _require_device(tensor: torch.Tensor, what: str) -> None:
+    lib()
+    if tensor.device.type != "cuda":
+        raise ValueError(f"{what} requires GPU tensors")
+    if not _device_is_gfx950(tensor.device.index if tensor.device.index is not None else torch.cuda.current_device()):
+        raise RuntimeError(f"{what}: the xblock kernels are built for gfx950 only")
+
+
+def _dtype_code(dtype: torch.dtype, what: str) -> int:
+    try:
+        return _DTYPE_CODES[dtype]
+    except KeyError:
+        raise ValueError(f"{what}: unsupported dtype {dtype}") from None
+
+
+def _ptr(tensor: Optional[torch.Tensor]) -> Optional[int]:
+    return None if tensor is None else tensor.data_ptr()
+
+
+def layer_norm(
+    inputs: torch.Tensor,
+    weight: torch.Tensor,
+    bias: torch.Tensor,
+    eps: float,
+    output_dtype: torch.dtype,
+    apply_affine: bool = True,
+) -> torch.Tensor:
+    """LayerNorm whose output is stored directly in the next GEMM's dtype (FN:140-170)."""
+    _require_device(inputs, "layer_norm")
+    n_cols = inputs.shape[-1]
+    if n_cols != weight.numel() or weight.shape != bias.shape:
+        raise ValueError("LayerNorm parameters do not match the input width")
+    if inputs.dtype != torch.float32:
+        raise ValueError("layer_norm expects float32 inputs")
+    inputs = inputs.contiguous()
+    output = torch.empty_like(inputs, dtype=output_dtype)
+    rows = inputs.numel() // n_cols
+    check(
+        lib().xb_layernorm(
+            inputs.data_ptr(), _ptr(weight), _ptr(bias), output.data_ptr(),
+            _dtype_code(output_dtype, "layer_norm"), rows, n_cols, float(eps),
+            int(bool(apply_affine)), stream_handle(inputs.device),
+        ),
+        "xb_layernorm",
+    )
+    return output
+
+
+def fused_residual_layer_norm(
+    residual: torch.Tensor,
+    update: torch.Tensor,
+    weight: torch.Tensor,
+    bias: torch.Tensor,
+    eps: float,
+    norm_dtype: torch.dtype,
+    store_residual: bool = True,
+    apply_affine: bool = True,
+    residual_out: Optional[torch.Tensor] = None,
+    norm_out: Optional[torch.Tensor] = None,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Return (residual + update in FP32, LayerNorm of it in `norm_dtype`) (FN:173-215).
+
+    With store_residual=False the sum is not written and the input `residual`
+    object is returned, as in the reference.  `residual_out` / `norm_out` let
+    a caller supply destinations (residual_out may be `residual` itself).
+    """
+    _require_device(residual, "fused_residual_layer_norm")
+    if residual.shape != update.shape:
+        raise ValueError("residual and update must have identical shapes")
+    if residual.shape[-1] != weight.numel() or weight.shape != bias.shape:
+        raise ValueError("LayerNorm parameters do not match the input width")
+    if residual.dtype != torch.float32:
+        raise ValueError("the residual stream must be float32")
+    if not residual.is_contiguous() or not update.is_contiguous():
+        raise ValueError("residual and update must be contiguous")
+    n_cols = residual.shape[-1]
+    if store_residual:
+        if residual_out is None:
+            residual_out = torch.empty_like(residual)
+    else:
+        residual_out = None
+    if norm_out is None:
+        norm_out = torch.empty_like(residual, dtype=norm_dtype)
+    rows = residual.numel() // n_cols
+    check(
+        lib().xb_residual_layernorm(
+            residual.data_ptr(), update.data_ptr(), _dtype_code(update.dtype, "update"),
+            _ptr(weight), _ptr(bias), _ptr(residual_out), norm_out.data_ptr(),
+            _dtype_code(norm_out.dtype, "norm"), rows, n_cols, float(eps),
+            int(bool(apply_affine)), stream_handle(residual.device),
+        ),
+        "xb_residual_layernorm",
+    )
+    return (residual_out if store_residual else residual), norm_out
+
+
+def linear(
+    inputs: torch.Tensor,
+    weight: torch.Tensor,
+    bias: Optional[torch.Tensor],
+    gelu: bool = False,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """FP16 `inputs @ weight.T + bias` (optionally exact-erf GELU), FP32 accumulation.
+
+    inputs: [..., K] float16 contiguous; weight: [N, K] float16 (nn.Linear
+    layout); bias: [N] float32 or None.  Returns [..., N] float16.
+    """
+    _require_device(inputs, "linear")
+    if weight.ndim != 2 or (bias is not None and bias.ndim != 1):
+        raise ValueError("weight must be 2-D and bias must be 1-D")
+    k = inputs.shape[-1]
+    n = weight.shape[0]
+    if weight.shape[1] != k:
+        raise ValueError("weight does not match the input width")
+    if bias is not None and (bias.numel() != n or bias.dtype != torch.float32):
+        raise ValueError("bias must be float32 with one entry per output feature")
+    if inputs.dtype != torch.float16 or weight.dtype != torch.float16:
+        raise ValueError("linear expects float16 inputs and weights")
+    if not inputs.is_contiguous() or not weight.is_contiguous():
+        raise ValueError("linear expects contiguous inputs and weights")
+    m = inputs.numel() // k
+    if out is None:
+        out = torch.empty((*inputs.shape[:-1], n), device=inputs.device, dtype=torch.float16)
+    check(
+        lib().xb_linear(
+            inputs.data_ptr(), weight.data_ptr(), _ptr(bias), out.data_ptr(), m, n, k,
+            XB_EPI_BIAS_GELU if gelu else XB_EPI_BIAS, stream_handle(inputs.device),
+        ),
+        "xb_linear",
+    )
+    return out
+
+
+def ffn_gelu(inputs: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
+    """GELU(inputs @ weight.T + bias) with FP32 accumulation (triton_fused_ffn.py:224-261).
+
+    Unlike the reference's tanh epilogue (triton_fused_ffn.py:205-213) this is
+    the exact-erf GELU of the baseline (torch_transformer_benchmark.py:286).
+    """
+    return linear(inputs, weight, bias, gelu=True)
+
+
+def causal_attention(
+    qkv: torch.Tensor,
+    num_heads: int,
+    scale: Optional[float] = None,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Causal attention over a packed [B, S, 3*D] FP16 projection -> [B, S, D] FP16.
+
+    Column j of the packed projection is (which, head, dim) with
+    which in (q, k, v), exactly the [B, S, 3, H, hd] view the reference takes
+    (torch_transformer_benchmark.py:742-745).  `scale` defaults to
+    head_dim ** -0.5, SDPA's default and the baseline's (TTB:215).
+    """
+    _require_device(qkv, "causal_attention")
+    if qkv.ndim != 3 or qkv.shape[-1] % (3 * num_heads) != 0:
+        raise ValueError("qkv must be [B, S, 3 * num_heads * head_dim]")
+    if qkv.dtype != torch.float16 or not qkv.is_contiguous():
+        raise ValueError("qkv must be contiguous float16")
+    batch, seq_len, width = qkv.shape
+    d_model = width // 3
+    head_dim = d_model // num_heads
+    if scale is None:
+        scale = head_dim ** -0.5
+    if out is None:
+        out = torch.empty((batch, seq_len, d_model), device=qkv.device, dtype=torch.float16)
+    check(
+        lib().xb_attention_causal(
+            qkv.data_ptr(), out.data_ptr(), batch, seq_len, num_heads, head_dim,
+            float(scale), stream_handle(qkv.device),
+        ),
+        "xb_attention_causal",
+    )
+    return out

@@ -1,0 +1,285 @@
+"""`UserOptimizedTransformer`: the drop-in causal pre-norm block stack on gfx950.
+
+The module tree reproduces the reference's exactly -- ``layers.{i}.norm1``,
+``layers.{i}.attention.{q,k,v,out}_proj``, ``layers.{i}.norm2``,
+``layers.{i}.ffn_in``, ``layers.{i}.ffn_out``, ``final_norm``
+(torch_transformer_benchmark.py:204-317) -- constructed in the same order, so
+a strict `load_state_dict` from the reference's `BaselineTransformer` works
+(torch_transformer_benchmark.py:1151-1161) and a seeded construction draws the
+same nn.Linear initialisation.
+
+`forward(x, valid_token_mask=None)` follows `_forward_cuda_fused_norm`
+(torch_transformer_benchmark.py:1092-1148) with every device op a HIP kernel
+from libxblock.so:
+
+    n1 = LN(x)                                       xb_layernorm
+    per layer:
+      qkv = n1 . Wqkv^T + bqkv                       xb_linear        [M, 3D] fp16
+      ctx = causal_attention(qkv)                    xb_attention     [M, D]  fp16
+      a   = ctx . Wo^T + bo                          xb_linear        [M, D]  fp16
+      x, n2 = x + a, LN2(x + a)                      xb_residual_layernorm
+      h   = gelu_erf(n2 . W1^T + b1)                 xb_linear(GELU)  [M, F]  fp16
+      f   = h . W2^T + b2                            xb_linear        [M, D]  fp16
+      x, n1 = x + f, LN(x + f)  (next norm1, or final_norm in FP32 for the last layer)
+
+The residual stream is FP32; GEMM operands are FP16 with FP32 accumulation,
+the storage scheme of the reference's mixed-precision path.  There is no CPU
+or PyTorch-op fallback: inputs that the HIP path cannot serve raise.
+"""
+
+from __future__ import annotations
+
+from typing import Dict, Optional, Tuple
+
+import torch
+import torch.nn as nn
+
+from . import kernels
+from .config import ShapeExecutionPlan, TransformerConfig, resolve_shape_execution_plan
+
+
+class SelfAttentionParameters(nn.Module):
+    """Parameter container with the reference's attention layout (TTB:207-220)."""
+
+    def __init__(self, d_model: int, num_heads: int) -> None:
+        super().__init__()
+        if d_model % num_heads != 0:
+            raise ValueError("d_model must be divisible by num_heads")
+        self.d_model = d_model
+        self.num_heads = num_heads
+        self.head_dim = d_model // num_heads
+        self.scale = self.head_dim**-0.5
+        self.q_proj = nn.Linear(d_model, d_model, bias=True)
+        self.k_proj = nn.Linear(d_model, d_model, bias=True)
+        self.v_proj = nn.Linear(d_model, d_model, bias=True)
+        self.out_proj = nn.Linear(d_model, d_model, bias=True)
+
+    def forward(self, *args, **kwargs):  # pragma: no cover - explicit guard
+        raise RuntimeError("run attention through UserOptimizedTransformer.forward")
+
+
+class TransformerBlockParameters(nn.Module):
+    """Parameter container with the reference's block layout (TTB:270-277)."""
+
+    def __init__(self, d_model: int, num_heads: int, ffn_dim: int) -> None:
+        super().__init__()
+        self.norm1 = nn.LayerNorm(d_model)
+        self.attention = SelfAttentionParameters(d_model, num_heads)
+        self.norm2 = nn.LayerNorm(d_model)
+        self.ffn_in = nn.Linear(d_model, ffn_dim)
+        self.ffn_out = nn.Linear(ffn_dim, d_model)
+
+    def forward(self, *args, **kwargs):  # pragma: no cover - explicit guard
+        raise RuntimeError("run blocks through UserOptimizedTransformer.forward")
+
+
+def _tensor_version(tensor: torch.Tensor) -> Optional[int]:
+    try:
+        return tensor._version
+    except RuntimeError:  # inference tensors expose no version counter
+        return None
+
+
+class _LayerWeights:
+    """FP16 GEMM operands and FP32 biases of one block, as the kernels want them."""
+
+    __slots__ = ("qkv_w", "qkv_b", "out_w", "out_b", "ffn_in_w", "ffn_in_b", "ffn_out_w", "ffn_out_b")
+
+    def __init__(self, layer: TransformerBlockParameters) -> None:
+        att = layer.attention
+        with torch.no_grad():
+            self.qkv_w = torch.cat((att.q_proj.weight, att.k_proj.weight, att.v_proj.weight), 0).to(torch.float16).contiguous()
+            self.qkv_b = torch.cat((att.q_proj.bias, att.k_proj.bias, att.v_proj.bias), 0).float().contiguous()
+            self.out_w = att.out_proj.weight.to(torch.float16).contiguous()
+            self.out_b = att.out_proj.bias.float().contiguous()
+            self.ffn_in_w = layer.ffn_in.weight.to(torch.float16).contiguous()
+            self.ffn_in_b = layer.ffn_in.bias.float().contiguous()
+            self.ffn_out_w = layer.ffn_out.weight.to(torch.float16).contiguous()
+            self.ffn_out_b = layer.ffn_out.bias.float().contiguous()
+
+
+class UserOptimizedTransformer(nn.Module):
+    """Drop-in for the reference's UserOptimizedTransformer (TTB:320-1148), HIP-only."""
+
+    def __init__(self, config: TransformerConfig) -> None:
+        super().__init__()
+        config.validate()
+        self.config = config
+        self.layers = nn.ModuleList(
+            [
+                TransformerBlockParameters(config.d_model, config.num_heads, config.ffn_dim)
+                for _ in range(config.num_layers)
+            ]
+        )
+        self.final_norm = nn.LayerNorm(config.d_model)
+        self._shape_execution_plan = resolve_shape_execution_plan(config)
+        # The gfx950 path computes GEMMs and attention in FP16 (FP32 accumulation,
+        # FP32 residual stream); the reference reaches the same state through
+        # enable_mixed_precision(torch.float16) (TTB:1750-1771).
+        self._mixed_precision_dtype: Optional[torch.dtype] = torch.float16
+        self._kv_cache_enabled = False
+        self._kv_cache_length = 0
+        self._large_batch_chunk_size = self._shape_execution_plan.batch_chunk_size
+
+    # ----------------------------------------------------------------- toggles
+    @property
+    def shape_execution_plan(self) -> ShapeExecutionPlan:
+        """The immutable dispatch decision (TTB:364-367)."""
+        return self._shape_execution_plan
+
+    def enable_mixed_precision(self, dtype: Optional[torch.dtype] = torch.float16) -> None:
+        """Select the compute dtype (TTB:369-377); the HIP path implements float16."""
+        if dtype not in (None, torch.float16, torch.bfloat16):
+            raise ValueError("mixed precision dtype must be float16 or bfloat16")
+        if self._kv_cache_length:
+            raise RuntimeError("reset the KV cache before changing precision")
+        self._mixed_precision_dtype = dtype
+
+    def enable_kv_cache(self, enabled: bool = True) -> None:
+        """KV-cached decoding (TTB:408-417) is not part of the HIP path."""
+        if enabled:
+            raise NotImplementedError("KV-cached decoding is not implemented by the gfx950 path")
+        self._kv_cache_enabled = False
+        self.reset_kv_cache()
+
+    def reset_kv_cache(self) -> None:
+        self._kv_cache_length = 0
+
+    @property
+    def kv_cache_length(self) -> int:
+        return self._kv_cache_length
+
+    # ------------------------------------------------------------ parameter caches
+    def _layer_weights(self, index: int) -> _LayerWeights:
+        """Packed FP16 weights, rebuilt when any source parameter changes (TTB:524-641)."""
+        layer = self.layers[index]
+        params = list(layer.attention.parameters()) + list(layer.ffn_in.parameters()) + list(layer.ffn_out.parameters())
+        key = tuple((p.data_ptr(), _tensor_version(p), p.device, p.dtype) for p in params)
+        cache: Dict[int, Tuple[tuple, _LayerWeights]] = self.__dict__.setdefault("_weight_cache", {})
+        cached = cache.get(index)
+        if cached is None or cached[0] != key or any(k[1] is None for k in key):
+            cached = (key, _LayerWeights(layer))
+            cache[index] = cached
+        return cached[1]
+
+    @staticmethod
+    def _layer_norm_uses_affine(layer_norm: nn.LayerNorm) -> bool:
+        """Whether gamma/beta differ from (1, 0), cached per version (TTB:568-596)."""
+        weight, bias = layer_norm.weight, layer_norm.bias
+        if weight is None or bias is None:
+            return False
+        versions = (_tensor_version(weight), _tensor_version(bias))
+        if None in versions:
+            return True
+        key = (weight.data_ptr(), versions[0], bias.data_ptr(), versions[1])
+        cached = getattr(layer_norm, "_xblock_affine_cache", None)
+        if cached is None or cached[0] != key:
+            with torch.no_grad():
+                is_identity = bool(torch.all(weight == 1).item()) and bool(torch.all(bias == 0).item())
+            cached = (key, not is_identity)
+            layer_norm._xblock_affine_cache = cached
+        return cached[1]
+
+    def _all_tokens_valid(self, valid_token_mask: Optional[torch.Tensor], seq_len: int) -> bool:
+        """Mask inspection cached by identity + version + length (TTB:464-522)."""
+        if valid_token_mask is None:
+            return True
+        version = _tensor_version(valid_token_mask)
+        cached = self.__dict__.get("_mask_cache")
+        if version is not None and cached is not None and cached[0] is valid_token_mask and cached[1] == version and cached[2] == seq_len:
+            return cached[3]
+        result = bool(valid_token_mask.all().item())
+        if version is not None:
+            self.__dict__["_mask_cache"] = (valid_token_mask, version, seq_len, result)
+        return result
+
+    # ----------------------------------------------------------------- forward
+    def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+        if x.device.type != "cuda":
+            raise RuntimeError(
+                "UserOptimizedTransformer runs only on the gfx950 HIP path; move the model and "
+                "input to the GPU (there is deliberately no CPU fallback)"
+            )
+        if self._mixed_precision_dtype != torch.float16:
+            raise NotImplementedError("the gfx950 path implements float16 compute only")
+        if not self.config.causal:
+            raise NotImplementedError("the gfx950 path implements causal attention only")
+        if x.ndim != 3 or x.shape[-1] != self.config.d_model:
+            raise ValueError(f"expected input [B, S, {self.config.d_model}], got {tuple(x.shape)}")
+        if x.dtype != torch.float32:
+            raise ValueError("the gfx950 path expects a float32 residual stream input")
+        if self.training:
+            raise RuntimeError("UserOptimizedTransformer is inference-only; call eval()")
+        if not self._all_tokens_valid(valid_token_mask, x.shape[1]):
+            raise NotImplementedError("padding masks are not implemented by the gfx950 path")
+        x = x.contiguous()
+        chunk = self._large_batch_chunk_size
+        with torch.no_grad():
+            if chunk and x.shape[0] > chunk:
+                output = torch.empty_like(x)
+                for start in range(0, x.shape[0], chunk):
+                    end = min(start + chunk, x.shape[0])
+                    self._forward_hip(x[start:end], out=output[start:end])
+                return output
+            return self._forward_hip(x)
+
+    def _forward_hip(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """The fused kernel sequence of TTB:1092-1148 for one all-valid causal batch."""
+        cfg = self.config
+        batch, seq_len, d_model = x.shape
+        rows = batch * seq_len
+        dev = x.device
+        f16 = torch.float16
+        num_layers = len(self.layers)
+
+        first = self.layers[0].norm1
+        norm = kernels.layer_norm(x, first.weight, first.bias, first.eps, f16, apply_affine=self._layer_norm_uses_affine(first))
+        residual_in = x
+        residual = torch.empty((batch, seq_len, d_model), device=dev, dtype=torch.float32)
+        if out is None:
+            out = torch.empty_like(x)
+        for index, layer in enumerate(self.layers):
+            w = self._layer_weights(index)
+            qkv = kernels.linear(norm, w.qkv_w, w.qkv_b)
+            context = kernels.causal_attention(qkv, cfg.num_heads, layer.attention.scale)
+            update = kernels.linear(context, w.out_w, w.out_b)
+            residual_in, norm2 = kernels.fused_residual_layer_norm(
+                residual_in, update, layer.norm2.weight, layer.norm2.bias, layer.norm2.eps, f16,
+                apply_affine=self._layer_norm_uses_affine(layer.norm2), residual_out=residual,
+            )
+            hidden = kernels.linear(norm2, w.ffn_in_w, w.ffn_in_b, gelu=True)
+            update = kernels.linear(hidden, w.ffn_out_w, w.ffn_out_b)
+            last = index == num_layers - 1
+            following = self.final_norm if last else self.layers[index + 1].norm1
+            residual_in, norm = kernels.fused_residual_layer_norm(
+                residual_in, update, following.weight, following.bias, following.eps,
+                torch.float32 if last else f16, store_residual=not last,
+                apply_affine=self._layer_norm_uses_affine(following),
+                residual_out=residual, norm_out=out if last else None,
+            )
+        return norm
+
+
+def forward_flops(config: TransformerConfig, batch: Optional[int] = None, seq_len: Optional[int] = None) -> float:
+    """GEMM + causal-attention FLOPs of one forward (2*B*S*L*(4D^2+2DF) + 2*B*L*D*S*(S+1))."""
+    b = config.batch_size if batch is None else batch
+    s = config.seq_len if seq_len is None else seq_len
+    d, f, layers = config.d_model, config.ffn_dim, config.num_layers
+    return 2.0 * b * s * layers * (4 * d * d + 2 * d * f) + 2.0 * b * layers * d * s * (s + 1)
+
+
+def forward_bytes(config: TransformerConfig, batch: Optional[int] = None, seq_len: Optional[int] = None) -> float:
+    """HBM bytes of the unfused kernel pipeline: B*S*(4D + L*(48D + 4F)) + 2*L*(4D^2 + 2DF)."""
+    b = config.batch_size if batch is None else batch
+    s = config.seq_len if seq_len is None else seq_len
+    d, f, layers = config.d_model, config.ffn_dim, config.num_layers
+    return b * s * (4 * d + layers * (48 * d + 4 * f)) + 2.0 * layers * (4 * d * d + 2 * d * f)
+
+
+__all__ = [
+    "SelfAttentionParameters",
+    "TransformerBlockParameters",
+    "UserOptimizedTransformer",
+    "forward_flops",
+    "forward_bytes",
+]

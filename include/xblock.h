@@ -1,0 +1,98 @@
+/*
+ * xblock: C-ABI of the MI355X (gfx950) kernels behind the causal pre-norm
+ * Transformer block inference path (UserOptimizedTransformer.forward).
+ *
+ * Conventions shared by every entry point:
+ *   - plain device pointers to caller-owned memory, element counts in int64/int32;
+ *   - `stream` is a hipStream_t passed as void* (NULL = the default stream);
+ *   - work is only enqueued: no allocation, no host synchronisation, so every
+ *     call is safe inside hipGraph stream capture;
+ *   - return 0 on success, a negative XB_ERR_* for a rejected argument (nothing
+ *     is launched), or a positive hipError_t from the launch.
+ * Reference citations are file:line inside gwenlim89/GPU-kernel-for-transformer.
+ */
+#ifndef XBLOCK_H
+#define XBLOCK_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define XB_ABI_VERSION 1
+
+/* Argument errors (negative); positive values are hipError_t codes. */
+#define XB_OK 0
+#define XB_ERR_NULL_POINTER (-1)
+#define XB_ERR_BAD_SIZE (-2)
+#define XB_ERR_BAD_DTYPE (-3)
+#define XB_ERR_UNSUPPORTED_SHAPE (-4)
+#define XB_ERR_MISALIGNED (-5)
+#define XB_ERR_BAD_EPILOGUE (-6)
+
+/* Element types of activations. */
+#define XB_F32 0
+#define XB_F16 1
+
+/* GEMM epilogues applied to (A . W^T + bias) before the FP16 store. */
+#define XB_EPI_BIAS 0       /* y = acc + bias                                  */
+#define XB_EPI_BIAS_GELU 1  /* y = gelu_erf(acc + bias) (exact erf, not tanh)  */
+
+int xb_abi_version(void);
+const char* xb_strerror(int code);
+
+/*
+ * y[r, :] = LayerNorm(x[r, :]) (* gamma + beta when apply_affine), FP32 math,
+ * biased variance, y stored as y_dtype.  x: [rows, cols] FP32, contiguous.
+ * Replaces layer_norm / _layer_norm_kernel (triton_fused_norm.py:140-170,
+ * triton_fused_norm.py:84-121), called for layer 0's norm1
+ * (torch_transformer_benchmark.py:1103-1111).
+ */
+int xb_layernorm(const float* x, const float* gamma, const float* beta, void* y,
+                 int y_dtype, int64_t rows, int32_t cols, float eps,
+                 int apply_affine, void* stream);
+
+/*
+ * s = residual + update (FP32); residual_out = s unless residual_out is NULL;
+ * y = LayerNorm(s) (* gamma + beta) stored as y_dtype.  residual_out may alias
+ * residual (in-place update of the residual stream).
+ * Replaces fused_residual_layer_norm / _residual_layer_norm_kernel
+ * (triton_fused_norm.py:173-215, triton_fused_norm.py:37-81); NULL
+ * residual_out is the reference's store_residual=False.
+ */
+int xb_residual_layernorm(const float* residual, const void* update,
+                          int update_dtype, const float* gamma,
+                          const float* beta, float* residual_out, void* y,
+                          int y_dtype, int64_t rows, int32_t cols, float eps,
+                          int apply_affine, void* stream);
+
+/*
+ * c[M, N] = epilogue(a[M, K] . w[N, K]^T + bias[N]) with FP16 operands, FP32
+ * MFMA accumulation and an FP16 store.  w is nn.Linear's own [out, in] layout;
+ * bias is FP32 (may be NULL for no bias).  K and N must be multiples of 8.
+ * Replaces F.linear under FP16 autocast (torch_transformer_benchmark.py:685,
+ * :741), triton_ffn_gelu (triton_fused_ffn.py:224-261) and the grouped
+ * accumulation kernels (triton_fused_ffn.py:264-411).
+ */
+int xb_linear(const void* a, const void* w, const float* bias, void* c,
+              int64_t m, int32_t n, int32_t k, int epilogue, void* stream);
+
+/*
+ * Causal multi-head attention over a packed projection.
+ * qkv: [batch, seq_len, 3, heads, head_dim] FP16 (the packed QKV GEMM output);
+ * out: [batch, seq_len, heads, head_dim] FP16 (= [B, S, D], ready for the
+ * output projection).  softmax(q k^T * scale, top-left causal) v with FP32
+ * online softmax.  head_dim in {8, 16, 32, 64, 128, 256}.
+ * Replaces F.scaled_dot_product_attention(is_causal=True) and the following
+ * transpose/reshape (torch_transformer_benchmark.py:742-809).
+ */
+int xb_attention_causal(const void* qkv, void* out, int32_t batch,
+                        int64_t seq_len, int32_t heads, int32_t head_dim,
+                        float scale, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* XBLOCK_H */

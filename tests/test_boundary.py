@@ -1,0 +1,128 @@
+"""CPU tests of the drop-in boundary: config type, state_dict compatibility,
+the C-ABI library's exports and argument checks, and the no-fallback rule."""
+
+from __future__ import annotations
+
+import ctypes
+import json
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from oracle.baseline import BaselineTransformer, copy_model_weights
+
+REPO = Path(__file__).resolve().parents[1]
+
+
+def test_config_validation_messages(pkg):
+    TC = pkg.TransformerConfig
+    TC(2, 4, 8, 2, 8, 1, True).validate()
+    with pytest.raises(ValueError, match="batch_size must be positive"):
+        TC(0, 4, 8, 2, 8, 1, True).validate()
+    with pytest.raises(ValueError, match=r"d_model \(10\) must be divisible by num_heads \(4\)"):
+        TC(1, 4, 10, 4, 8, 1, True).validate()
+    with pytest.raises(ValueError, match="num_layers must be positive"):
+        TC(1, 4, 8, 2, 8, 0, True).validate()
+    assert hash(TC(1, 2, 8, 2, 8, 1, True)) == hash(TC(1, 2, 8, 2, 8, 1, True))
+
+
+def test_benchmark_configs_match_baseline_json(pkg):
+    """BASELINE.json's five configs are official shapes 1, 6, 8, 11, 14."""
+    configs = json.loads((REPO / "BASELINE.json").read_text())["configs"]
+    assert len(configs) == 5
+    expected = [(64, 128, 128, 4, 128, 4), (10000, 128, 128, 4, 128, 4), (64, 128, 1024, 4, 1024, 4),
+                (64, 128, 128, 16, 128, 4), (32, 100000, 1024, 16, 1024, 2)]
+    for shape_id, geom in zip(pkg.BENCHMARK_CONFIG_SHAPE_IDS, expected):
+        c = pkg.OFFICIAL_BENCHMARK_SHAPES[shape_id]
+        assert (c.batch_size, c.seq_len, c.d_model, c.num_heads, c.ffn_dim, c.num_layers) == geom
+        assert c.causal
+    assert "B=10000" in configs[1] and "head_dim 8" in configs[3] and "S=100000" in configs[4]
+
+
+def test_shape_plan(pkg):
+    plan = pkg.resolve_shape_execution_plan(pkg.OFFICIAL_BENCHMARK_SHAPES[6])
+    assert plan.official_shape_id == 6
+    assert plan.describe().startswith("official-6: ffn=")
+    general = pkg.resolve_shape_execution_plan(pkg.TransformerConfig(3, 5, 8, 2, 8, 1, True))
+    assert general.official_shape_id is None and general.describe().startswith("general:")
+
+
+@pytest.mark.parametrize("geom", [(2, 8, 32, 4, 48, 2), (1, 4, 128, 16, 128, 1)])
+def test_state_dict_is_the_baselines(pkg, geom):
+    cfg = pkg.TransformerConfig(*geom, True)
+    torch.manual_seed(1234)
+    baseline = BaselineTransformer(cfg)
+    torch.manual_seed(1234)
+    optimized = pkg.UserOptimizedTransformer(cfg)
+    assert list(baseline.state_dict().keys()) == list(optimized.state_dict().keys())
+    # Same construction order => the same seeded nn.Linear initialisation.
+    for (k, a), (_, b) in zip(baseline.state_dict().items(), optimized.state_dict().items()):
+        assert torch.equal(a, b), k
+    other = pkg.UserOptimizedTransformer(cfg)
+    copy_model_weights(baseline, other)  # strict load_state_dict (TTB:1151-1161)
+    for (k, a), (_, b) in zip(baseline.state_dict().items(), other.state_dict().items()):
+        assert torch.equal(a, b), k
+
+
+def test_forward_has_no_cpu_fallback(pkg):
+    cfg = pkg.TransformerConfig(1, 4, 32, 4, 32, 1, True)
+    model = pkg.UserOptimizedTransformer(cfg).eval()
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        model(torch.randn(1, 4, 32))
+
+
+def test_toggles(pkg):
+    model = pkg.UserOptimizedTransformer(pkg.TransformerConfig(1, 4, 32, 4, 32, 1, True))
+    with pytest.raises(ValueError):
+        model.enable_mixed_precision(torch.float32)
+    model.enable_mixed_precision(torch.float16)
+    with pytest.raises(NotImplementedError):
+        model.enable_kv_cache(True)
+    model.enable_kv_cache(False)
+    assert model.kv_cache_length == 0
+    assert model.shape_execution_plan.official_shape_id is None
+
+
+def test_product_never_touches_the_oracle():
+    for path in (REPO / "gpu-kernel-for-transformer_amd").rglob("*.py"):
+        text = path.read_text()
+        assert not re.search(r"^\s*(from|import)\s+oracle", text, re.M), path
+
+
+# ----------------------------------------------------------------------------- C-ABI
+def _declared_symbols():
+    header = (REPO / "include" / "xblock.h").read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(xb_\w+)\s*\(", header, re.M)))
+
+
+def test_library_exports_every_declared_symbol(capi):
+    assert capi.XBLOCK_AVAILABLE, capi.XBLOCK_LOAD_ERROR
+    declared = _declared_symbols()
+    assert declared == sorted(capi.EXPORTED_SYMBOLS)
+    handle = ctypes.CDLL(str(capi.LIBRARY_PATH))
+    for name in declared:
+        assert hasattr(handle, name), name
+    assert capi.lib().xb_abi_version() == capi.XB_ABI_VERSION
+
+
+def test_argument_errors_need_no_gpu(capi):
+    lib = capi.lib()
+    assert lib.xb_linear(None, None, None, None, 4, 8, 8, 0, None) == -1
+    assert lib.xb_linear(None, None, None, None, 0, 8, 8, 0, None) == 0   # empty: NULL allowed
+    assert lib.xb_layernorm(None, None, None, None, 1, 0, 128, 1e-5, 0, None) == 0
+    assert lib.xb_linear(16, 16, None, 16, 4, 7, 8, 0, None) == -4      # N % 8
+    assert lib.xb_linear(16, 16, None, 16, 4, 8, 8, 9, None) == -6      # epilogue
+    assert lib.xb_linear(18, 16, None, 16, 4, 8, 8, 0, None) == -5      # alignment
+    assert lib.xb_linear(16, 16, None, 16, 0, 8, 8, 0, None) == 0       # empty: no launch
+    assert lib.xb_layernorm(16, None, None, 16, 7, 4, 128, 1e-5, 0, None) == -3
+    assert lib.xb_layernorm(16, None, None, 16, 1, -1, 128, 1e-5, 0, None) == -2
+    assert lib.xb_layernorm(16, None, None, 16, 1, 4, 128, 1e-5, 1, None) == -1  # affine w/o gamma
+    assert lib.xb_residual_layernorm(16, 16, 1, None, None, None, 16, 1, 0, 128, 1e-5, 0, None) == 0
+    assert lib.xb_attention_causal(16, 16, 1, 8, 2, 24, 0.1, None) == -4  # head_dim 24
+    assert lib.xb_attention_causal(16, 16, 0, 8, 2, 8, 0.1, None) == 0
+    for code in (0, -1, -2, -3, -4, -5, -6):
+        assert lib.xb_strerror(code)
+    with pytest.raises(RuntimeError, match="xb_linear failed with code -4"):
+        capi.check(-4, "xb_linear")

@@ -1,0 +1,154 @@
+"""Per-kernel parity of the HIP kernels against plain PyTorch FP32 references.
+
+Every reference is computed on the CPU in FP32 from the same (FP16-rounded,
+where the kernel takes FP16) inputs.  Tolerances, stated per test, allow for
+the kernels' FP16 output rounding (2^-11 relative) and FP32 summation order.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+pytestmark = pytest.mark.gpu
+
+F16, F32 = torch.float16, torch.float32
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+# ----------------------------------------------------------------------------- LayerNorm
+@pytest.mark.parametrize("rows,cols", [(0, 128), (1, 128), (7, 128), (8192, 128), (33, 1024), (5, 64), (3, 96), (2, 2048), (4, 768), (3, 256), (9, 512), (2, 1000)])
+@pytest.mark.parametrize("out_dtype", [F16, F32])
+@pytest.mark.parametrize("affine", [False, True])
+def test_layer_norm(pkg, cuda, rows, cols, out_dtype, affine):
+    x = torch.randn(rows, cols, generator=_gen(rows * 7 + cols)) * 2.0 + 0.5
+    g = torch.randn(cols, generator=_gen(1)) * 0.3 + 1.0
+    b = torch.randn(cols, generator=_gen(2)) * 0.1
+    y = pkg.layer_norm(x.to(cuda), g.to(cuda), b.to(cuda), 1e-5, out_dtype, apply_affine=affine)
+    ref = F.layer_norm(x, (cols,), g if affine else None, b if affine else None, 1e-5)
+    assert y.dtype == out_dtype and y.shape == x.shape
+    if out_dtype == F32:
+        torch.testing.assert_close(y.cpu(), ref, atol=2e-5, rtol=2e-5)
+    else:  # within one FP16 ulp of the rounded reference
+        torch.testing.assert_close(y.cpu().float(), ref.half().float(), atol=2e-3, rtol=1e-3)
+
+
+@pytest.mark.parametrize("cols", [128, 1024, 96])
+@pytest.mark.parametrize("upd_dtype", [F16, F32])
+@pytest.mark.parametrize("mode", ["store", "inplace", "nostore_f32"])
+def test_fused_residual_layer_norm(pkg, cuda, cols, upd_dtype, mode):
+    rows = 517
+    r = torch.randn(rows, cols, generator=_gen(3)) * 1.5
+    u = (torch.randn(rows, cols, generator=_gen(4)) * 0.7).to(upd_dtype)
+    g = torch.randn(cols, generator=_gen(5)) * 0.3 + 1.0
+    b = torch.randn(cols, generator=_gen(6)) * 0.1
+    s = r + u.float()
+    ref = F.layer_norm(s, (cols,), g, b, 1e-5)
+    rg, ug = r.to(cuda), u.to(cuda)
+    if mode == "store":
+        res, norm = pkg.fused_residual_layer_norm(rg, ug, g.to(cuda), b.to(cuda), 1e-5, F16)
+        torch.testing.assert_close(res.cpu(), s, atol=0, rtol=0)
+        torch.testing.assert_close(rg.cpu(), r, atol=0, rtol=0)  # input untouched
+        torch.testing.assert_close(norm.cpu().float(), ref.half().float(), atol=2e-3, rtol=1e-3)
+    elif mode == "inplace":
+        res, norm = pkg.fused_residual_layer_norm(rg, ug, g.to(cuda), b.to(cuda), 1e-5, F16, residual_out=rg)
+        assert res.data_ptr() == rg.data_ptr()
+        torch.testing.assert_close(rg.cpu(), s, atol=0, rtol=0)
+        torch.testing.assert_close(norm.cpu().float(), ref.half().float(), atol=2e-3, rtol=1e-3)
+    else:
+        res, norm = pkg.fused_residual_layer_norm(rg, ug, g.to(cuda), b.to(cuda), 1e-5, F32, store_residual=False)
+        assert res is rg
+        torch.testing.assert_close(rg.cpu(), r, atol=0, rtol=0)
+        torch.testing.assert_close(norm.cpu(), ref, atol=2e-5, rtol=2e-5)
+
+
+def test_layer_norm_errors(pkg, cuda):
+    x = torch.randn(4, 128, device=cuda)
+    with pytest.raises(ValueError):
+        pkg.layer_norm(x, torch.ones(64, device=cuda), torch.zeros(64, device=cuda), 1e-5, F16)
+    with pytest.raises(ValueError):
+        pkg.fused_residual_layer_norm(x, torch.zeros(4, 64, device=cuda), torch.ones(128, device=cuda), torch.zeros(128, device=cuda), 1e-5, F16)
+    with pytest.raises(ValueError):
+        pkg.layer_norm(x.cpu(), torch.ones(128), torch.zeros(128), 1e-5, F16)
+
+
+# ----------------------------------------------------------------------------- GEMM
+@pytest.mark.parametrize(
+    "m,n,k",
+    [(1, 128, 128), (7, 384, 128), (8192, 384, 128), (8192, 128, 128), (1000, 1024, 1024),
+     (8192, 3072, 1024), (257, 136, 72), (64, 8, 8), (300, 1024, 128), (131072, 384, 128)],
+)
+@pytest.mark.parametrize("gelu", [False, True])
+def test_linear(pkg, cuda, m, n, k, gelu):
+    a = torch.randn(m, k, generator=_gen(m + n)).half()
+    w = (torch.randn(n, k, generator=_gen(k)) * k**-0.5).half()
+    bias = torch.randn(n, generator=_gen(n)) * 0.1
+    ref = a.float() @ w.float().T + bias
+    if gelu:
+        ref = F.gelu(ref, approximate="none")
+    out = pkg.linear(a.to(cuda), w.to(cuda), bias.to(cuda), gelu=gelu)
+    assert out.dtype == F16 and out.shape == (m, n)
+    # FP16 store (2^-11 relative) plus FP32 accumulation-order noise.
+    torch.testing.assert_close(out.cpu().float(), ref, atol=2e-3, rtol=2e-3)
+
+
+def test_linear_without_bias_and_batched_shape(pkg, cuda):
+    a = torch.randn(3, 5, 64, generator=_gen(1)).half()
+    w = (torch.randn(32, 64, generator=_gen(2)) * 0.125).half()
+    out = pkg.linear(a.to(cuda), w.to(cuda), None)
+    assert out.shape == (3, 5, 32)
+    torch.testing.assert_close(out.cpu().float(), a.float() @ w.float().T, atol=2e-3, rtol=2e-3)
+
+
+def test_linear_errors(pkg, cuda):
+    a = torch.randn(4, 64, device=cuda).half()
+    with pytest.raises(ValueError):
+        pkg.linear(a, torch.randn(32, 48, device=cuda).half(), None)
+    with pytest.raises(ValueError):
+        pkg.linear(a.float(), torch.randn(32, 64, device=cuda).half(), None)
+    with pytest.raises(RuntimeError, match="code -4"):
+        pkg.linear(torch.randn(4, 60, device=cuda).half(), torch.randn(32, 60, device=cuda).half(), None)
+
+
+# ----------------------------------------------------------------------------- attention
+def _attention_reference(qkv: torch.Tensor, heads: int) -> torch.Tensor:
+    b, s, width = qkv.shape
+    d = width // 3
+    hd = d // heads
+    t = qkv.float().view(b, s, 3, heads, hd).permute(2, 0, 3, 1, 4)
+    q, k, v = t[0], t[1], t[2]
+    scores = (q @ k.transpose(-2, -1)) * hd**-0.5
+    scores = scores.masked_fill(torch.ones(s, s, dtype=torch.bool).triu(1), float("-inf"))
+    return (torch.softmax(scores, -1) @ v).transpose(1, 2).reshape(b, s, d)
+
+
+@pytest.mark.parametrize("hd", [8, 16, 32, 64, 128, 256])
+@pytest.mark.parametrize("b,s,h", [(2, 1, 2), (1, 17, 2), (2, 128, 4), (1, 200, 2), (1, 333, 1)])
+def test_causal_attention(pkg, cuda, hd, b, s, h):
+    qkv = torch.randn(b, s, 3 * h * hd, generator=_gen(hd * 1000 + s)).half()
+    ref = _attention_reference(qkv, h)
+    out = pkg.causal_attention(qkv.to(cuda), h)
+    assert out.dtype == F16 and out.shape == (b, s, h * hd)
+    # FP16 probabilities and FP16 output rounding.
+    torch.testing.assert_close(out.cpu().float(), ref, atol=2e-3, rtol=1e-2)
+
+
+@pytest.mark.parametrize("hd,s", [(64, 4096), (8, 1500), (256, 700)])
+def test_causal_attention_long(pkg, cuda, hd, s):
+    h = 2 if hd < 256 else 1
+    qkv = torch.randn(1, s, 3 * h * hd, generator=_gen(s)).half()
+    ref = _attention_reference(qkv, h)
+    out = pkg.causal_attention(qkv.to(cuda), h)
+    torch.testing.assert_close(out.cpu().float(), ref, atol=2e-3, rtol=1e-2)
+
+
+def test_causal_attention_first_token_is_value(pkg, cuda):
+    """Query 0 sees only key 0, so its context equals v[0] exactly (up to FP16)."""
+    qkv = torch.randn(3, 50, 3 * 4 * 32, generator=_gen(9)).half()
+    out = pkg.causal_attention(qkv.to(cuda), 4).cpu()
+    v0 = qkv[:, 0, 2 * 128:].float()
+    torch.testing.assert_close(out[:, 0].float(), v0, atol=1e-3, rtol=1e-3)
