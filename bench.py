@@ -1,0 +1,275 @@
+#!/usr/bin/env python3
+"""Throughput of the MI355X causal pre-norm block inference path.
+
+Headline workload (the BASELINE metric's config that fits one GPU):
+BASELINE config 2 = official shape 6, B=10000 S=128 D=128 H=4 F=128 L=4, one
+"step" = one full forward of the whole batch with the input resident in HBM.
+Weights: nn.Linear default init under torch.manual_seed(1234) (random, no
+checkpoint); input: x ~ N(0,1) from seed 1234+100000 (synthetic), as the
+reference's benchmark draws it (torch_transformer_benchmark.py:1478-1485).
+
+Printed as ONE JSON line with, besides the driver's fields:
+  roofline      the dominant kernel (largest share of step time), timed with
+                HIP events around each of its launches inside the timed steps
+                (on the launch stream), against its algorithmic bytes or FLOPs
+  cpu_baseline  the CPU FP32 oracle (restated BaselineTransformer) on a bounded
+                sample of the same workload, on this host's cores; its outputs
+                double as the accuracy check of the GPU output on that sample
+  per_config    tokens/s, ms and roofline fraction for all five BASELINE
+                configs, each with its accuracy result on a bounded sample
+Only one GPU is used; --gpus above 1 exits with an explanation.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+HBM_BYTES_PER_S = 8.0e12          # MI355X HBM3E peak
+FP16_MFMA_FLOPS = 2.5166e15       # MI355X dense FP16 MFMA peak (256 CU x 2.4 GHz x 4096)
+CONFIG_NAMES = {1: "cfg1", 6: "cfg2", 8: "cfg3", 11: "cfg4", 14: "cfg5"}
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=10)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--workload", type=int, default=6, choices=sorted(CONFIG_NAMES), help="official shape id of the headline line")
+    p.add_argument("--no-per-config", action="store_true", help="skip the other four configs")
+    p.add_argument("--cpu-seconds", type=float, default=15.0, help="bound on the CPU baseline's timed work")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--profile-only", action="store_true", help="only the headline timed steps (for rocprofv3)")
+    return p.parse_args()
+
+
+def kernel_costs(name: str, config, rows: int):
+    """Algorithmic (bytes, flops) of ONE launch of kernel `name` on `rows` tokens."""
+    d, f, s = config.d_model, config.ffn_dim, config.seq_len
+    b = rows // s
+    if name.startswith("layernorm"):
+        return rows * 6 * d, 0.0
+    if name.startswith("residual_layernorm"):
+        return rows * (10 if name.endswith("_final") else 12) * d, 0.0
+    if name.startswith("attention"):
+        return rows * 8 * d, 2.0 * b * d * s * (s + 1)
+    if name.startswith("gemm_"):
+        parts = name.split("_")
+        n, k = int(parts[1][1:]), int(parts[2][1:])
+        return rows * 2 * (n + k) + 2 * n * k, 2.0 * rows * n * k
+    raise KeyError(name)
+
+
+def roofline_of(bytes_, flops, seconds):
+    t_hbm, t_mfma = bytes_ / HBM_BYTES_PER_S, flops / FP16_MFMA_FLOPS
+    if t_mfma > t_hbm:
+        achieved = flops / seconds / 1e12
+        return {"bound": "mfma", "achieved": achieved, "peak": FP16_MFMA_FLOPS / 1e12, "unit": "TFLOP/s", "frac": achieved * 1e12 / FP16_MFMA_FLOPS}
+    achieved = bytes_ / seconds / 1e9
+    return {"bound": "hbm", "achieved": achieved, "peak": HBM_BYTES_PER_S / 1e9, "unit": "GB/s", "frac": achieved * 1e9 / HBM_BYTES_PER_S}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one MI355X only: this build has no multi-GPU path "
+              "(the batch shards with no exchange step; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+    import __graft_entry__ as entry
+
+    pkg = entry.load_package()
+    kernels = __import__(pkg.__name__ + ".kernels", fromlist=["LaunchRecorder"])
+    graphs = __import__(pkg.__name__ + ".graph_runner", fromlist=["FixedInputCUDAGraph"])
+    if not pkg.XBLOCK_AVAILABLE:
+        raise RuntimeError(f"libxblock.so unavailable: {pkg.XBLOCK_LOAD_ERROR}")
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+
+    def build(config):
+        from oracle.baseline import BaselineTransformer, copy_model_weights
+
+        torch.manual_seed(1234)
+        baseline = BaselineTransformer(config).eval()
+        model = pkg.UserOptimizedTransformer(config)
+        copy_model_weights(baseline, model)
+        return baseline, model.to(device).eval()
+
+    def make_input(config, seed):
+        g = torch.Generator(device=device).manual_seed(seed)
+        return torch.randn(config.batch_size, config.seq_len, config.d_model, generator=g, device=device)
+
+    def time_steps(run, steps, warmup):
+        for _ in range(warmup):
+            run()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(steps):
+            run()
+        end.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        return start.elapsed_time(end) / steps, wall
+
+    def cpu_leg(baseline, config, gpu_out, x_gpu, budget_s, rows_per_call):
+        """Oracle on the host cores over a bounded slice; returns rate and accuracy."""
+        from oracle.accuracy import compare_outputs
+
+        threads = torch.get_num_threads()
+        x_cpu = x_gpu[:rows_per_call].float().cpu()
+        prefix = None
+        if config.seq_len > 8192:  # long context: causal prefix only
+            prefix = 4096
+            x_cpu = x_gpu[:rows_per_call, :prefix].float().cpu()
+        with torch.inference_mode():
+            t0 = time.perf_counter()
+            ref = baseline(x_cpu)
+            first = time.perf_counter() - t0
+            calls, elapsed = 1, first
+            while elapsed < budget_s * 0.5 and elapsed + first < budget_s:
+                t1 = time.perf_counter()
+                baseline(x_cpu)
+                elapsed += time.perf_counter() - t1
+                calls += 1
+        tokens = calls * x_cpu.shape[0] * x_cpu.shape[1]
+        cand = gpu_out[:rows_per_call] if prefix is None else gpu_out[:rows_per_call, :prefix]
+        acc = compare_outputs(ref, cand.cpu())
+        sample = f"{x_cpu.shape[0]} x {x_cpu.shape[1]} tokens per call, {calls} calls" + (
+            f" (causal prefix {prefix} of S={config.seq_len})" if prefix else "")
+        return {"value": tokens / elapsed, "unit": "tokens/s", "cores": threads, "kind": "port", "sample": sample}, acc
+
+    results = {}
+    order = [args.workload] + ([] if (args.no_per_config or args.profile_only) else [i for i in CONFIG_NAMES if i != args.workload])
+    headline = None
+    for shape_id in order:
+        config = pkg.OFFICIAL_BENCHMARK_SHAPES[shape_id]
+        name = CONFIG_NAMES[shape_id]
+        log(f"[bench] {name} (official shape {shape_id}): {config}")
+        baseline, model = build(config)
+        x = make_input(config, 1234 + 100000)
+        tokens = config.batch_size * config.seq_len
+        big = config.seq_len > 8192
+        is_head = shape_id == args.workload
+        if big:
+            steps, warmup = (max(1, min(args.steps, 3)), 1) if is_head else (2, 1)
+        else:
+            steps, warmup = (args.steps, args.warmup) if is_head else (20, 5)
+        with torch.inference_mode():
+            if big or tokens >= 1_000_000:
+                run = lambda: model(x)  # noqa: E731  (launch-overhead-free at this size)
+                mode = "eager"
+            else:
+                graphed = graphs.FixedInputCUDAGraph(model, x, None)
+                run = lambda: graphed(x)  # noqa: E731  (clone included, as the reference's replay)
+                mode = "hipGraph replay"
+            ms, wall = time_steps(run, steps, warmup)
+            out = model(x)
+            torch.cuda.synchronize()
+        entry_ = {
+            "workload": name, "official_shape": shape_id, "tokens_per_s": tokens / (ms / 1e3), "ms": ms,
+            "mode": mode, "steps": steps,
+        }
+        fl, by = pkg.forward_flops(config), pkg.forward_bytes(config)
+        t_bound = max(fl / FP16_MFMA_FLOPS, by / HBM_BYTES_PER_S)
+        entry_["bound"] = "mfma" if fl / FP16_MFMA_FLOPS > by / HBM_BYTES_PER_S else "hbm"
+        entry_["roofline_frac"] = t_bound / (ms / 1e3)
+        log(f"[bench] {name}: {ms:.3f} ms/step, {entry_['tokens_per_s']:.4g} tokens/s ({mode}), roofline frac {entry_['roofline_frac']:.3f}")
+
+        if is_head:
+            headline = dict(entry_, config=config, wall=wall)
+            if not args.profile_only:
+                # Per-kernel durations with HIP events inside timed eager steps.
+                with torch.inference_mode(), kernels.LaunchRecorder() as rec:
+                    for _ in range(max(2, min(steps, 5))):
+                        model(x)
+                torch.cuda.synchronize()
+                per = {}
+                for kname, durs in rec.durations_ms().items():
+                    avg = statistics.fmean(durs)
+                    b_, f_ = kernel_costs(kname, config, tokens)
+                    per[kname] = {"avg_ms": avg, "launches_per_step": len(durs) // max(2, min(steps, 5)),
+                                  "share_ms": avg * len(durs) / max(2, min(steps, 5)), **roofline_of(b_, f_, avg / 1e3),
+                                  "bytes_per_launch": b_, "flops_per_launch": f_}
+                dominant = max(per, key=lambda k: per[k]["share_ms"])
+                headline["kernels"] = per
+                headline["dominant"] = dominant
+                for kname, v in sorted(per.items(), key=lambda kv: -kv[1]["share_ms"]):
+                    log(f"[bench]   {kname:28s} {v['avg_ms']*1e3:9.1f} us x{v['launches_per_step']} "
+                        f"{v['achieved']:9.1f} {v['unit']} ({v['frac']*100:5.1f}% {v['bound']})")
+
+        if not args.profile_only:
+            if args.no_cpu_baseline and not is_head:
+                pass
+            else:
+                rows = {1: 64, 6: 256, 8: 16, 11: 64, 14: 1}[shape_id]
+                budget = args.cpu_seconds if is_head else min(args.cpu_seconds, 5.0)
+                if args.no_cpu_baseline:
+                    budget = 0.0
+                cpu, acc = cpu_leg(baseline, config, out, x, budget, rows)
+                entry_["accuracy"] = {"failed": acc.failed_elements, "total": acc.total_elements,
+                                      "max_abs": acc.max_abs_error, "passed": acc.passed}
+                entry_["cpu_baseline_tokens_per_s"] = cpu["value"]
+                log(f"[bench] {name}: accuracy {acc.summary()}; CPU FP32 oracle {cpu['value']:.4g} tokens/s on {cpu['cores']} threads ({cpu['sample']})")
+                if is_head:
+                    headline["cpu_baseline"] = cpu
+                    headline["accuracy"] = entry_["accuracy"]
+        results[name] = entry_
+        del baseline, model, x, out
+        torch.cuda.empty_cache()
+
+    cfg = headline["config"]
+    line = {
+        "metric": "tokens/sec per config on 1 MI355X; % of FP16 MFMA / HBM roofline",
+        "value": headline["tokens_per_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": headline["steps"],
+        "warmup": args.warmup,
+        "ms_per_step": headline["ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (x ~ N(0,1) seeded; nn.Linear default init, seed 1234)",
+        "config": {
+            "workload": f"{CONFIG_NAMES[args.workload]}: official shape {args.workload}, causal pre-norm block forward",
+            "batch": cfg.batch_size, "seq_len": cfg.seq_len, "d_model": cfg.d_model, "heads": cfg.num_heads,
+            "ffn_dim": cfg.ffn_dim, "layers": cfg.num_layers, "mode": headline["mode"],
+        },
+        "roofline_frac_forward": headline["roofline_frac"],
+    }
+    if "dominant" in headline:
+        k = headline["kernels"][headline["dominant"]]
+        line["roofline"] = {
+            "kernel": headline["dominant"], "bound": k["bound"], "achieved": k["achieved"], "peak": k["peak"],
+            "unit": k["unit"], "frac": k["frac"], "traffic": None, "avg_us": k["avg_ms"] * 1e3,
+            "bytes_per_launch": k["bytes_per_launch"], "flops_per_launch": k["flops_per_launch"],
+        }
+        line["kernels"] = {n: {"avg_us": round(v["avg_ms"] * 1e3, 2), "per_step": v["launches_per_step"],
+                               "frac": round(v["frac"], 4), "bound": v["bound"]} for n, v in headline["kernels"].items()}
+    if "cpu_baseline" in headline:
+        line["cpu_baseline"] = headline["cpu_baseline"]
+        line["accuracy"] = headline["accuracy"]
+    if len(results) > 1:
+        line["per_config"] = {n: {k: (round(v, 6) if isinstance(v, float) else v) for k, v in r.items()} for n, r in results.items()}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

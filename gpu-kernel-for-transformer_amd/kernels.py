@@ -16,7 +16,7 @@ on torch's current stream, and never synchronise: they are capture-safe.
 from __future__ import annotations
 
 from functools import lru_cache
-from typing import Optional, Tuple
+from typing import Callable, Dict, List, Optional, Tuple
 
 import torch
 
@@ -24,6 +24,46 @@ from . import _capi
 from ._capi import XB_EPI_BIAS, XB_EPI_BIAS_GELU, XB_F16, XB_F32, check, lib, stream_handle
 
 _DTYPE_CODES = {torch.float32: XB_F32, torch.float16: XB_F16}
+
+
+class LaunchRecorder:
+    """Opt-in per-launch timing: brackets every kernel launch with HIP events.
+
+    Used by bench.py to measure each kernel's average duration inside the timed
+    region, on the stream the kernel is launched on.  While no recorder is
+    active a launch costs one `is None` check.
+
+        with LaunchRecorder() as rec:
+            model(x)
+        torch.cuda.synchronize(); rec.durations_ms() -> {name: [ms, ...]}
+    """
+
+    _active: Optional["LaunchRecorder"] = None
+
+    def __init__(self) -> None:
+        self.events: Dict[str, List[Tuple[torch.cuda.Event, torch.cuda.Event]]] = {}
+
+    def __enter__(self) -> "LaunchRecorder":
+        LaunchRecorder._active = self
+        return self
+
+    def __exit__(self, *exc) -> None:
+        LaunchRecorder._active = None
+
+    def durations_ms(self) -> Dict[str, List[float]]:
+        return {name: [a.elapsed_time(b) for a, b in pairs] for name, pairs in self.events.items()}
+
+
+def _launch(name: str, fn: Callable[[], int]) -> int:
+    recorder = LaunchRecorder._active
+    if recorder is None:
+        return fn()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    code = fn()
+    end.record()
+    recorder.events.setdefault(name, []).append((start, end))
+    return code
 
 
 @lru_cache(maxsize=None)
@@ -68,12 +108,12 @@ def layer_norm(
     inputs = inputs.contiguous()
     output = torch.empty_like(inputs, dtype=output_dtype)
     rows = inputs.numel() // n_cols
+    code = _dtype_code(output_dtype, "layer_norm")
     check(
-        lib().xb_layernorm(
-            inputs.data_ptr(), _ptr(weight), _ptr(bias), output.data_ptr(),
-            _dtype_code(output_dtype, "layer_norm"), rows, n_cols, float(eps),
-            int(bool(apply_affine)), stream_handle(inputs.device),
-        ),
+        _launch(f"layernorm_{n_cols}", lambda: lib().xb_layernorm(
+            inputs.data_ptr(), _ptr(weight), _ptr(bias), output.data_ptr(), code, rows, n_cols,
+            float(eps), int(bool(apply_affine)), stream_handle(inputs.device),
+        )),
         "xb_layernorm",
     )
     return output
@@ -115,13 +155,14 @@ def fused_residual_layer_norm(
     if norm_out is None:
         norm_out = torch.empty_like(residual, dtype=norm_dtype)
     rows = residual.numel() // n_cols
+    upd_code, norm_code = _dtype_code(update.dtype, "update"), _dtype_code(norm_out.dtype, "norm")
+    name = f"residual_layernorm_{n_cols}{'' if store_residual else '_final'}"
     check(
-        lib().xb_residual_layernorm(
-            residual.data_ptr(), update.data_ptr(), _dtype_code(update.dtype, "update"),
-            _ptr(weight), _ptr(bias), _ptr(residual_out), norm_out.data_ptr(),
-            _dtype_code(norm_out.dtype, "norm"), rows, n_cols, float(eps),
+        _launch(name, lambda: lib().xb_residual_layernorm(
+            residual.data_ptr(), update.data_ptr(), upd_code, _ptr(weight), _ptr(bias),
+            _ptr(residual_out), norm_out.data_ptr(), norm_code, rows, n_cols, float(eps),
             int(bool(apply_affine)), stream_handle(residual.device),
-        ),
+        )),
         "xb_residual_layernorm",
     )
     return (residual_out if store_residual else residual), norm_out
@@ -155,11 +196,12 @@ def linear(
     m = inputs.numel() // k
     if out is None:
         out = torch.empty((*inputs.shape[:-1], n), device=inputs.device, dtype=torch.float16)
+    epi = XB_EPI_BIAS_GELU if gelu else XB_EPI_BIAS
     check(
-        lib().xb_linear(
-            inputs.data_ptr(), weight.data_ptr(), _ptr(bias), out.data_ptr(), m, n, k,
-            XB_EPI_BIAS_GELU if gelu else XB_EPI_BIAS, stream_handle(inputs.device),
-        ),
+        _launch(f"gemm_n{n}_k{k}{'_gelu' if gelu else ''}", lambda: lib().xb_linear(
+            inputs.data_ptr(), weight.data_ptr(), _ptr(bias), out.data_ptr(), m, n, k, epi,
+            stream_handle(inputs.device),
+        )),
         "xb_linear",
     )
     return out
@@ -200,10 +242,10 @@ def causal_attention(
     if out is None:
         out = torch.empty((batch, seq_len, d_model), device=qkv.device, dtype=torch.float16)
     check(
-        lib().xb_attention_causal(
-            qkv.data_ptr(), out.data_ptr(), batch, seq_len, num_heads, head_dim,
-            float(scale), stream_handle(qkv.device),
-        ),
+        _launch(f"attention_hd{head_dim}", lambda: lib().xb_attention_causal(
+            qkv.data_ptr(), out.data_ptr(), batch, seq_len, num_heads, head_dim, float(scale),
+            stream_handle(qkv.device),
+        )),
         "xb_attention_causal",
     )
     return out
