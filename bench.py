@@ -61,6 +61,11 @@ def kernel_costs(name: str, config, rows: int):
         return rows * (10 if name.endswith("_final") else 12) * d, 0.0
     if name.startswith("attention"):
         return rows * 8 * d, 2.0 * b * d * s * (s + 1)
+    if name == "fused_forward_d128":
+        layers = config.num_layers
+        weights = 2 * layers * (4 * d * d + 2 * d * f)
+        attn = 2.0 * b * layers * d * s * (s + 1)
+        return rows * 8 * d + weights, 2.0 * rows * layers * (4 * d * d + 2 * d * f) + attn
     if name.startswith("gemm_"):
         parts = name.split("_")
         n, k = int(parts[1][1:]), int(parts[2][1:])

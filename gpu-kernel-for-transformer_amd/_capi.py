@@ -30,6 +30,8 @@ XB_F32 = 0
 XB_F16 = 1
 XB_EPI_BIAS = 0
 XB_EPI_BIAS_GELU = 1
+XB_PACK_PERMUTED = 0
+XB_PACK_NATURAL = 1
 
 EXPORTED_SYMBOLS = (
     "xb_abi_version",
@@ -38,6 +40,8 @@ EXPORTED_SYMBOLS = (
     "xb_residual_layernorm",
     "xb_linear",
     "xb_attention_causal",
+    "xb_pack_linear_fragments",
+    "xb_fused_forward_d128",
 )
 
 _vp = ctypes.c_void_p
@@ -54,6 +58,8 @@ _SIGNATURES = {
     ),
     "xb_linear": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, ctypes.c_int, _vp]),
     "xb_attention_causal": (ctypes.c_int, [_vp, _vp, _i32, _i64, _i32, _i32, _f32, _vp]),
+    "xb_pack_linear_fragments": (ctypes.c_int, [_vp, _vp, _i32, _i32, _i32, _vp]),
+    "xb_fused_forward_d128": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _f32, _vp]),
 }
 
 _LIB: Optional[ctypes.CDLL] = None

@@ -249,3 +249,53 @@ def causal_attention(
         "xb_attention_causal",
     )
     return out
+
+
+def pack_linear_fragments(weight: torch.Tensor, natural: bool = False) -> torch.Tensor:
+    """FP16 fragment-major copy of an nn.Linear weight [n, k] for the fused kernel.
+
+    natural=False gives the permuted k order used against register-resident
+    activations, natural=True the plain order used against LDS-resident ones.
+    """
+    _require_device(weight, "pack_linear_fragments")
+    if weight.ndim != 2:
+        raise ValueError("weight must be 2-D")
+    w = weight.detach().float().contiguous()
+    n, k = w.shape
+    out = torch.empty(n * k, device=w.device, dtype=torch.float16)
+    check(
+        _launch("pack_fragments", lambda: lib().xb_pack_linear_fragments(
+            w.data_ptr(), out.data_ptr(), n, k, _capi.XB_PACK_NATURAL if natural else _capi.XB_PACK_PERMUTED,
+            stream_handle(w.device))),
+        "xb_pack_linear_fragments",
+    )
+    return out
+
+
+FUSED_D128_HEAD_DIMS = (8, 16, 32, 64, 128)
+
+
+def fused_forward_d128(
+    x: torch.Tensor,
+    wpack: torch.Tensor,
+    ppack: torch.Tensor,
+    num_heads: int,
+    ffn_dim: int,
+    num_layers: int,
+    scale: float,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Whole-stack forward for d_model 128 / seq_len <= 128 (see xb_fused_forward_d128)."""
+    _require_device(x, "fused_forward_d128")
+    if x.ndim != 3 or x.shape[-1] != 128 or x.dtype != torch.float32 or not x.is_contiguous():
+        raise ValueError("x must be contiguous float32 [B, S, 128]")
+    batch, seq_len, _ = x.shape
+    if out is None:
+        out = torch.empty_like(x)
+    check(
+        _launch("fused_forward_d128", lambda: lib().xb_fused_forward_d128(
+            x.data_ptr(), out.data_ptr(), wpack.data_ptr(), ppack.data_ptr(), batch, seq_len,
+            num_heads, ffn_dim, num_layers, float(scale), stream_handle(x.device))),
+        "xb_fused_forward_d128",
+    )
+    return out

@@ -120,6 +120,7 @@ class UserOptimizedTransformer(nn.Module):
         self._kv_cache_enabled = False
         self._kv_cache_length = 0
         self._large_batch_chunk_size = self._shape_execution_plan.batch_chunk_size
+        self._fused_stack_enabled = True
 
     # ----------------------------------------------------------------- toggles
     @property
@@ -134,6 +135,14 @@ class UserOptimizedTransformer(nn.Module):
         if self._kv_cache_length:
             raise RuntimeError("reset the KV cache before changing precision")
         self._mixed_precision_dtype = dtype
+
+    def enable_fused_stack(self, enabled: bool = True) -> None:
+        """Use the one-kernel whole-stack forward where its shape contract holds.
+
+        With it disabled every shape runs the per-op kernel sequence; the two
+        paths compute the same math (FP16 operands, FP32 accumulation).
+        """
+        self._fused_stack_enabled = bool(enabled)
 
     def enable_kv_cache(self, enabled: bool = True) -> None:
         """KV-cached decoding (TTB:408-417) is not part of the HIP path."""
@@ -161,6 +170,42 @@ class UserOptimizedTransformer(nn.Module):
             cached = (key, _LayerWeights(layer))
             cache[index] = cached
         return cached[1]
+
+    def _uses_fused_stack(self, x: torch.Tensor) -> bool:
+        """Shape contract of xb_fused_forward_d128."""
+        cfg = self.config
+        norms = [m for m in self.modules() if isinstance(m, nn.LayerNorm)]
+        return (
+            self._fused_stack_enabled
+            and cfg.d_model == 128
+            and cfg.ffn_dim == 128
+            and x.shape[1] <= 128
+            and cfg.head_dim in kernels.FUSED_D128_HEAD_DIMS
+            and all(n.eps == 1e-5 and n.weight is not None and n.bias is not None for n in norms)
+        )
+
+    def _fused_stack_parameters(self) -> Tuple[torch.Tensor, torch.Tensor]:
+        """Fragment-packed FP16 weights and FP32 bias/LayerNorm buffer, cached by version."""
+        params = list(self.parameters())
+        key = tuple((p.data_ptr(), _tensor_version(p), p.device) for p in params)
+        cached = self.__dict__.get("_fused_stack_cache")
+        if cached is not None and cached[0] == key and all(k[1] is not None for k in key):
+            return cached[1], cached[2]
+        weights, vectors = [], []
+        with torch.no_grad():
+            for layer in self.layers:
+                att = layer.attention
+                for lin in (att.q_proj, att.k_proj, att.v_proj, att.out_proj, layer.ffn_in, layer.ffn_out):
+                    weights.append(kernels.pack_linear_fragments(lin.weight, natural=lin is att.out_proj))
+                for vec in (att.q_proj.bias, att.k_proj.bias, att.v_proj.bias, att.out_proj.bias,
+                            layer.ffn_in.bias, layer.ffn_out.bias, layer.norm1.weight, layer.norm1.bias,
+                            layer.norm2.weight, layer.norm2.bias):
+                    vectors.append(vec.detach().float().reshape(-1))
+            vectors += [self.final_norm.weight.detach().float(), self.final_norm.bias.detach().float()]
+            wpack = torch.cat(weights).contiguous()
+            ppack = torch.cat(vectors).contiguous()
+        self.__dict__["_fused_stack_cache"] = (key, wpack, ppack)
+        return wpack, ppack
 
     @staticmethod
     def _layer_norm_uses_affine(layer_norm: nn.LayerNorm) -> bool:
@@ -226,6 +271,12 @@ class UserOptimizedTransformer(nn.Module):
     def _forward_hip(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
         """The fused kernel sequence of TTB:1092-1148 for one all-valid causal batch."""
         cfg = self.config
+        if self._uses_fused_stack(x):
+            wpack, ppack = self._fused_stack_parameters()
+            return kernels.fused_forward_d128(
+                x, wpack, ppack, cfg.num_heads, cfg.ffn_dim, len(self.layers),
+                self.layers[0].attention.scale, out=out,
+            )
         batch, seq_len, d_model = x.shape
         rows = batch * seq_len
         dev = x.device

@@ -91,6 +91,42 @@ int xb_attention_causal(const void* qkv, void* out, int32_t batch,
                         int64_t seq_len, int32_t heads, int32_t head_dim,
                         float scale, void* stream);
 
+/* Fragment orders of xb_pack_linear_fragments. */
+#define XB_PACK_PERMUTED 0  /* k = 32*ks + 4*(l/16) + (m & 3) + 16*(m >> 2) */
+#define XB_PACK_NATURAL 1   /* k = 32*ks + 8*(l/16) + m                      */
+
+/*
+ * Packs an FP32 nn.Linear weight w[n, k] (n % 16 == 0, k % 32 == 0) into the
+ * FP16 fragment-major order xb_fused_forward_d128 streams its weights in:
+ *   out[((ob * (k/32) + ks) * 64 + l) * 8 + m] = w[16*ob + l%16][k(ks, l, m)]
+ * with k(ks, l, m) given by `order` (one 16-byte MFMA operand per lane, 1 KiB
+ * per 16x32 block).  Replaces the reference's cached weight conversions
+ * (_cached_linear_parameters / _packed_qkv, torch_transformer_benchmark.py:540-641).
+ */
+int xb_pack_linear_fragments(const float* w, void* out, int32_t n, int32_t k,
+                             int32_t order, void* stream);
+
+/*
+ * The whole forward (every layer and the final LayerNorm) for d_model == 128,
+ * seq_len <= 128, ffn_dim == 128, head_dim in {8, 16, 32, 64, 128}, LayerNorm
+ * eps 1e-5: one workgroup per sequence keeps the residual stream in registers,
+ * so x [batch, seq_len, 128] FP32 is read once and y (same shape, FP32) is
+ * written once.  Same math as the per-op sequence above (FP16 MFMA operands,
+ * FP32 accumulation / residual / softmax, exact-erf GELU).
+ *   wpack: per layer, fragment-packed (xb_pack_linear_fragments) Wq, Wk, Wv,
+ *          Wo [128,128], W1 [ffn,128], W2 [128,ffn], layers back to back; Wo
+ *          in XB_PACK_NATURAL order, the others in XB_PACK_PERMUTED order;
+ *   ppack: FP32, per layer bq, bk, bv, bo [128], b1 [ffn], b2 [128],
+ *          norm1 gamma, beta, norm2 gamma, beta [128 each]; then final_norm
+ *          gamma, beta.
+ * Replaces _forward_cuda_fused_norm (torch_transformer_benchmark.py:1092-1148)
+ * for the official d_model = 128 shapes.
+ */
+int xb_fused_forward_d128(const float* x, float* y, const void* wpack,
+                          const float* ppack, int64_t batch, int32_t seq_len,
+                          int32_t heads, int32_t ffn_dim, int32_t layers,
+                          float scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

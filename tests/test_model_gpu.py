@@ -39,27 +39,80 @@ def _check(reference, candidate, label):
     return result
 
 
+@pytest.mark.parametrize("fused", [True, False])
 @pytest.mark.parametrize("shape_id", [1, 8, 11])
-def test_config_parity_two_trials(pkg, cuda, shape_id):
+def test_config_parity_two_trials(pkg, cuda, shape_id, fused):
     config = pkg.OFFICIAL_BENCHMARK_SHAPES[shape_id]
     baseline, optimized = _models(pkg, config, cuda)
+    optimized.enable_fused_stack(fused)
     for trial in range(2):
         x, mask = generate_random_case(config, torch.device("cpu"), torch.float32, seed=1234 + trial)
         with torch.inference_mode():
             ref = baseline(x, mask)
             out = optimized(x.to(cuda), mask.to(cuda)).cpu()
-        _check(ref, out, f"shape {shape_id} trial {trial}")
+        _check(ref, out, f"shape {shape_id} fused={fused} trial {trial}")
 
 
-def test_config2_batch_10000_slices(pkg, cuda):
+@pytest.mark.parametrize("fused", [True, False])
+def test_config2_batch_10000_slices(pkg, cuda, fused):
     config = pkg.OFFICIAL_BENCHMARK_SHAPES[6]
     baseline, optimized = _models(pkg, config, cuda)
+    optimized.enable_fused_stack(fused)
     x, mask = generate_random_case(config, torch.device("cpu"), torch.float32, seed=1234)
     with torch.inference_mode():
         out = optimized(x.to(cuda), mask.to(cuda)).cpu()
         for start, end in ((0, 48), (5000, 5032), (10000 - 48, 10000)):
             ref = baseline(x[start:end], mask[start:end])
-            _check(ref, out[start:end], f"shape 6 rows {start}:{end}")
+            _check(ref, out[start:end], f"shape 6 fused={fused} rows {start}:{end}")
+
+
+@pytest.mark.parametrize(
+    "geom",
+    [(3, 128, 128, 4, 128, 4), (2, 128, 128, 16, 128, 2), (2, 128, 128, 1, 128, 1), (2, 128, 128, 2, 128, 2),
+     (2, 100, 128, 8, 128, 3), (5, 17, 128, 4, 128, 2), (4, 1, 128, 16, 128, 2), (2, 64, 128, 16, 128, 1),
+     (3, 33, 128, 8, 128, 1)],
+)
+def test_fused_stack_parity(pkg, cuda, geom):
+    """The one-kernel stack (D=128, S<=128) against the oracle, every head width, ragged S."""
+    config = pkg.TransformerConfig(*geom, True)
+    baseline, optimized = _models(pkg, config, cuda)
+    with torch.no_grad():
+        g = torch.Generator().manual_seed(11)
+        for name, p in baseline.named_parameters():
+            if "norm" in name:
+                p.copy_(torch.randn(p.shape, generator=g) * 0.2 + (1.0 if name.endswith("weight") else 0.0))
+    copy_model_weights(baseline, optimized)
+    x, mask = generate_random_case(config, torch.device("cpu"), torch.float32, seed=21)
+    xg = x.to(cuda)
+    assert optimized._uses_fused_stack(xg)
+    with torch.inference_mode():
+        ref = baseline(x, mask)
+        fused = optimized(xg).cpu()
+        optimized.enable_fused_stack(False)
+        unfused = optimized(xg).cpu()
+    _check(ref, fused, f"fused {geom}")
+    _check(ref, unfused, f"unfused {geom}")
+    torch.testing.assert_close(fused, unfused, atol=3e-3, rtol=1e-2)
+
+
+def test_pack_linear_fragments_layout(pkg, cuda):
+    """Bit-exact check of the fragment-major packing formula on the CPU."""
+    kernels = __import__(pkg.__name__ + ".kernels", fromlist=["pack_linear_fragments"])
+    n, k = 48, 96
+    w = torch.randn(n, k, generator=torch.Generator().manual_seed(2))
+    wh = w.half()
+    for natural in (False, True):
+        packed = kernels.pack_linear_fragments(w.to(cuda), natural=natural).cpu()
+        expect = torch.empty(n * k, dtype=torch.float16)
+        idx = 0
+        for ob in range(n // 16):
+            for ks in range(k // 32):
+                for lane in range(64):
+                    for m in range(8):
+                        col = 32 * ks + (8 * (lane // 16) + m if natural else 4 * (lane // 16) + (m & 3) + 16 * (m >> 2))
+                        expect[idx] = wh[16 * ob + lane % 16, col]
+                        idx += 1
+        assert torch.equal(packed, expect), f"natural={natural}"
 
 
 def test_config5_full_length_prefix(pkg, cuda):

@@ -214,3 +214,26 @@ def test_generate_random_case_contract():
     assert int(lengths.min()) >= round(32 * 0.75) and int(lengths.max()) <= 32
     assert bool((xp[~mp] == 0).all())
     assert bool(mp[:, 0].all())
+
+
+# ----------------------------------------------------------------------------- GELU approximation
+def _gelu_as7126(x: np.ndarray) -> np.ndarray:
+    """float64 restatement of the device GELU (common.h): A&S 7.1.26 erfc."""
+    p, a = 0.3275911, (0.254829592, -0.284496736, 1.421413741, -1.453152027, 1.061405429)
+    z = np.abs(x) / math.sqrt(2.0)
+    t = 1.0 / (1.0 + p * z)
+    poly = t * (a[0] + t * (a[1] + t * (a[2] + t * (a[3] + t * a[4]))))
+    half_erfc = 0.5 * poly * np.exp(-z * z)
+    return x * np.where(x >= 0, 1.0 - half_erfc, half_erfc)
+
+
+def test_gelu_approximation_error_bound():
+    """A&S 7.1.26 |erf error| <= 1.5e-7 => |gelu error| <= 0.75e-7 * |x| against exact erf."""
+    x = np.linspace(-12.0, 12.0, 200001)
+    exact = numpy_ref.gelu_erf(x)
+    err = np.abs(_gelu_as7126(x) - exact)
+    assert np.all(err <= 0.75e-7 * np.abs(x) + 1e-15)
+    assert err.max() < 1e-6  # far below one FP16 ulp of the stored activation
+    # and it is not the tanh form the reference's Triton epilogue used (max gap 4.7e-4)
+    tanh_form = 0.5 * x * (1 + np.tanh(math.sqrt(2 / math.pi) * (x + 0.044715 * x**3)))
+    assert np.abs(tanh_form - exact).max() > 1e-4
