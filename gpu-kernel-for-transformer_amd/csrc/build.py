@@ -40,8 +40,17 @@ def _hipcc() -> str:
     return found
 
 
+# Per-file additions.  The attention kernels mask with -inf and never see
+# NaN, so they drop IEEE NaN handling: max/min then compile to a single
+# v_max/v_min instead of a canonicalising pair.
+EXTRA_FLAGS = {
+    "fused_d128.hip": ["-fno-honor-nans"],
+    "attention.hip": ["-fno-honor-nans"],
+}
+
+
 def _compile(src: Path, obj: Path) -> None:
-    cmd = [_hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [_hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{proc.stderr}")

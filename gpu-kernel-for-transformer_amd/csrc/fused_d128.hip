@@ -141,7 +141,7 @@ __device__ __forceinline__ void gemm_accumulate(const half_t* __restrict__ w, co
 template <int HD>
 __global__ __launch_bounds__(256, 1) void fused_stack_kernel(
     const float* __restrict__ x, float* __restrict__ y, const half_t* __restrict__ wpack,
-    const float* __restrict__ ppack, int S, int layers, float scale_log2) {
+    const float* __restrict__ ppack, int S, int layers) {
   constexpr int F = 128;  // ffn_dim (the packed-layer strides below assume it)
   constexpr int H = D / HD;
   constexpr int FKS = F / 32;
@@ -156,6 +156,10 @@ __global__ __launch_bounds__(256, 1) void fused_stack_kernel(
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int g = lane / 16, r16 = lane % 16;
   const int tb0 = wave, tb1 = 7 - wave;
+  // Additive causal mask of a diagonal 16x16 block: key 4g + i vs query r16.
+  float4_t diag_mask;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) diag_mask[i] = (4 * g + i > r16) ? -INFINITY : 0.f;
   const int64_t seq = blockIdx.x;
   const float* xs = x + seq * S * D;
   float* ys = y + seq * S * D;
@@ -211,33 +215,33 @@ __global__ __launch_bounds__(256, 1) void fused_stack_kernel(
        for (int j = 0; j < PF; ++j) {
         const int ob = ob0 + j;
         const half8_t (&cur)[KS] = wcur[j];
-        float4_t a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
         if (ob < 2 * FB) {
           // Q / K: swapped product, lane = (token r16, features 16fb + 4g + i).
+          // Q's weights and bias arrive pre-multiplied by scale * log2(e).
+          const float4_t b = ld4(bqkv + 16 * ob + 4 * g);
+          float4_t a0 = b, a1 = b;
 #pragma unroll
           for (int ks = 0; ks < KS; ++ks) {
             a0 = mfma16x16x32(cur[ks], xn[0][ks], a0);
             a1 = mfma16x16x32(cur[ks], xn[1][ks], a1);
           }
           const int fb = ob % FB;
-          const float4_t b = ld4(bqkv + 16 * ob + 4 * g);
-          const float sc = ob < FB ? scale_log2 : 1.0f;  // softmax scale * log2(e) folded into Q
           half_t* dst = ob < FB ? q_lds : k_lds;
-          *reinterpret_cast<half4_t*>(dst + (16 * tb0 + r16) * LD + 16 * fb + 4 * g) = to_half4((a0 + b) * sc);
-          *reinterpret_cast<half4_t*>(dst + (16 * tb1 + r16) * LD + 16 * fb + 4 * g) = to_half4((a1 + b) * sc);
+          *reinterpret_cast<half4_t*>(dst + (16 * tb0 + r16) * LD + 16 * fb + 4 * g) = to_half4(a0);
+          *reinterpret_cast<half4_t*>(dst + (16 * tb1 + r16) * LD + 16 * fb + 4 * g) = to_half4(a1);
         } else {
           // V: unswapped product, lane = (tokens 16tb + 4g + i, feature 16fb + r16),
           // i.e. four consecutive entries of one V^T row.
+          const float bv = bqkv[16 * ob + r16];
+          float4_t a0 = {bv, bv, bv, bv}, a1 = a0;
 #pragma unroll
           for (int ks = 0; ks < KS; ++ks) {
             a0 = mfma16x16x32(xn[0][ks], cur[ks], a0);
             a1 = mfma16x16x32(xn[1][ks], cur[ks], a1);
           }
           const int fb = ob - 2 * FB;
-          const float bv = bqkv[16 * ob + r16];
-          const float4_t b = {bv, bv, bv, bv};
-          *reinterpret_cast<half4_t*>(vt_lds + (16 * fb + r16) * LD + 16 * tb0 + 4 * g) = to_half4(a0 + b);
-          *reinterpret_cast<half4_t*>(vt_lds + (16 * fb + r16) * LD + 16 * tb1 + 4 * g) = to_half4(a1 + b);
+          *reinterpret_cast<half4_t*>(vt_lds + (16 * fb + r16) * LD + 16 * tb0 + 4 * g) = to_half4(a0);
+          *reinterpret_cast<half4_t*>(vt_lds + (16 * fb + r16) * LD + 16 * tb1 + 4 * g) = to_half4(a1);
         }
        }
       }
@@ -250,7 +254,8 @@ __global__ __launch_bounds__(256, 1) void fused_stack_kernel(
     // ---- causal attention of the wave's query blocks, every head ------------
     // S^T = K . Q^T (M = keys, N = queries): lane holds keys 16kb + 4g + i of
     // query r16, which with the key order 32kt + 4g + (m&3) + 16(m>>2) is the
-    // B operand of O^T = V^T . P^T directly.
+    // B operand of O^T = V^T . P^T directly.  S <= 128 keys, so all scores of a
+    // query block fit in registers and the softmax needs no running rescale.
 #pragma unroll 1
     for (int t = 0; t < 2; ++t) {
       const int qb = t ? tb1 : tb0;
@@ -281,11 +286,7 @@ __global__ __launch_bounds__(256, 1) void fused_stack_kernel(
                   *reinterpret_cast<const half8_t*>(k_lds + (16 * kb + r16) * LD + 32 * (ks0 + j) + 8 * g);
               acc = mfma16x16x32(kf, qh[j], acc);
             }
-            if (kb == qb) {
-#pragma unroll
-              for (int i = 0; i < 4; ++i)
-                if (16 * kb + 4 * g + i > query) acc[i] = -INFINITY;
-            }
+            if (kb == qb) acc += diag_mask;  // -inf above the diagonal
             s[kb] = acc;
             mx = fmaxf(mx, fmaxf(fmaxf(acc[0], acc[1]), fmaxf(acc[2], acc[3])));
           }
@@ -360,15 +361,13 @@ __global__ __launch_bounds__(256, 1) void fused_stack_kernel(
 #pragma unroll
           for (int ks = 0; ks < KS; ++ks) wbuf1[ob % PF][ks] = frag(w1, (ob + PF) * KS + ks, lane);
         }
-        float4_t a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
+        const float4_t b = ld4(b1 + 16 * ob + 4 * g);
+        float4_t a0 = b, a1 = b;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
           a0 = mfma16x16x32(cur[ks], xn[0][ks], a0);
           a1 = mfma16x16x32(cur[ks], xn[1][ks], a1);
         }
-        const float4_t b = ld4(b1 + 16 * ob + 4 * g);
-        a0 += b;
-        a1 += b;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           hf[0][ob / 2][(ob & 1) * 4 + i] = (half_t)gelu_erf(a0[i]);
@@ -404,7 +403,7 @@ __global__ __launch_bounds__(256, 1) void fused_stack_kernel(
 // Fragment-major FP16 packing of an nn.Linear weight [n, k] (FP32 source).
 // permuted: k index 32ks + 4(l/16) + (m&3) + 16(m>>2); natural: 32ks + 8(l/16) + m.
 __global__ void pack_fragments_kernel(const float* __restrict__ w, half_t* __restrict__ out, int n, int k,
-                                      int permuted) {
+                                      int permuted, float scale) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t total = (int64_t)n * k;
   if (idx >= total) return;
@@ -416,14 +415,18 @@ __global__ void pack_fragments_kernel(const float* __restrict__ w, half_t* __res
   const int ob = frag_id / kss;
   const int row = 16 * ob + l % 16;
   const int col = permuted ? 32 * ks + 4 * (l / 16) + (m & 3) + 16 * (m >> 2) : 32 * ks + 8 * (l / 16) + m;
-  out[idx] = (half_t)w[(int64_t)row * k + col];
+  // Round the FP32 product to FP16 (two roundings, as the host computes it).
+  // The empty asm pins the FP32 value so the backend cannot fold multiply and
+  // convert into one singly-rounded v_fma_mix.
+  float v = w[(int64_t)row * k + col] * scale;
+  asm volatile("" : "+v"(v));
+  out[idx] = (half_t)v;
 }
 
 template <int HD>
 static hipError_t launch(const float* x, float* y, const half_t* w, const float* p, int64_t batch, int S,
-                         int layers, float scale_log2, hipStream_t s) {
-  hipLaunchKernelGGL((fused_stack_kernel<HD>), dim3((unsigned)batch), dim3(256), 0, s, x, y, w, p, S, layers,
-                     scale_log2);
+                         int layers, hipStream_t s) {
+  hipLaunchKernelGGL((fused_stack_kernel<HD>), dim3((unsigned)batch), dim3(256), 0, s, x, y, w, p, S, layers);
   return hipGetLastError();
 }
 
@@ -433,7 +436,7 @@ static hipError_t launch(const float* x, float* y, const half_t* w, const float*
 using namespace xb;
 
 extern "C" int xb_pack_linear_fragments(const float* w, void* out, int32_t n, int32_t k, int32_t order,
-                                        void* stream) {
+                                        float scale, void* stream) {
   if (n <= 0 || k <= 0) return XB_ERR_BAD_SIZE;
   if (n % 16 != 0 || k % 32 != 0) return XB_ERR_UNSUPPORTED_SHAPE;
   if (order != XB_PACK_PERMUTED && order != XB_PACK_NATURAL) return XB_ERR_BAD_EPILOGUE;
@@ -442,13 +445,13 @@ extern "C" int xb_pack_linear_fragments(const float* w, void* out, int32_t n, in
   const int64_t total = (int64_t)n * k;
   hipLaunchKernelGGL(fused::pack_fragments_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), w, static_cast<half_t*>(out), n, k,
-                     order == XB_PACK_PERMUTED ? 1 : 0);
+                     order == XB_PACK_PERMUTED ? 1 : 0, scale);
   return (int)hipGetLastError();
 }
 
 extern "C" int xb_fused_forward_d128(const float* x, float* y, const void* wpack, const float* ppack,
                                      int64_t batch, int32_t seq_len, int32_t heads, int32_t ffn_dim,
-                                     int32_t layers, float scale, void* stream) {
+                                     int32_t layers, void* stream) {
   if (batch < 0 || seq_len <= 0 || heads <= 0 || ffn_dim <= 0 || layers <= 0) return XB_ERR_BAD_SIZE;
   if (batch > 0x7fffffffLL) return XB_ERR_BAD_SIZE;
   if (seq_len > fused::SMAX || fused::D % heads != 0) return XB_ERR_UNSUPPORTED_SHAPE;
@@ -460,14 +463,13 @@ extern "C" int xb_fused_forward_d128(const float* x, float* y, const void* wpack
   if (((uintptr_t)x | (uintptr_t)y | (uintptr_t)wpack | (uintptr_t)ppack) & 15u) return XB_ERR_MISALIGNED;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const half_t* w = static_cast<const half_t*>(wpack);
-  const float sl2 = scale * 1.44269504088896340736f;
   hipError_t e;
   switch (hd) {
-    case 8: e = fused::launch<8>(x, y, w, ppack, batch, seq_len, layers, sl2, s); break;
-    case 16: e = fused::launch<16>(x, y, w, ppack, batch, seq_len, layers, sl2, s); break;
-    case 32: e = fused::launch<32>(x, y, w, ppack, batch, seq_len, layers, sl2, s); break;
-    case 64: e = fused::launch<64>(x, y, w, ppack, batch, seq_len, layers, sl2, s); break;
-    default: e = fused::launch<128>(x, y, w, ppack, batch, seq_len, layers, sl2, s); break;
+    case 8: e = fused::launch<8>(x, y, w, ppack, batch, seq_len, layers, s); break;
+    case 16: e = fused::launch<16>(x, y, w, ppack, batch, seq_len, layers, s); break;
+    case 32: e = fused::launch<32>(x, y, w, ppack, batch, seq_len, layers, s); break;
+    case 64: e = fused::launch<64>(x, y, w, ppack, batch, seq_len, layers, s); break;
+    default: e = fused::launch<128>(x, y, w, ppack, batch, seq_len, layers, s); break;
   }
   return (int)e;
 }

@@ -251,8 +251,8 @@ def causal_attention(
     return out
 
 
-def pack_linear_fragments(weight: torch.Tensor, natural: bool = False) -> torch.Tensor:
-    """FP16 fragment-major copy of an nn.Linear weight [n, k] for the fused kernel.
+def pack_linear_fragments(weight: torch.Tensor, natural: bool = False, scale: float = 1.0) -> torch.Tensor:
+    """FP16 fragment-major copy of `scale * weight` (nn.Linear [n, k]) for the fused kernel.
 
     natural=False gives the permuted k order used against register-resident
     activations, natural=True the plain order used against LDS-resident ones.
@@ -266,7 +266,7 @@ def pack_linear_fragments(weight: torch.Tensor, natural: bool = False) -> torch.
     check(
         _launch("pack_fragments", lambda: lib().xb_pack_linear_fragments(
             w.data_ptr(), out.data_ptr(), n, k, _capi.XB_PACK_NATURAL if natural else _capi.XB_PACK_PERMUTED,
-            stream_handle(w.device))),
+            float(scale), stream_handle(w.device))),
         "xb_pack_linear_fragments",
     )
     return out
@@ -282,10 +282,13 @@ def fused_forward_d128(
     num_heads: int,
     ffn_dim: int,
     num_layers: int,
-    scale: float,
     out: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
-    """Whole-stack forward for d_model 128 / seq_len <= 128 (see xb_fused_forward_d128)."""
+    """Whole-stack forward for d_model 128 / seq_len <= 128 (see xb_fused_forward_d128).
+
+    wpack / ppack come from UserOptimizedTransformer._fused_stack_parameters
+    (Wq and bq pre-multiplied by head_dim**-0.5 * log2(e)).
+    """
     _require_device(x, "fused_forward_d128")
     if x.ndim != 3 or x.shape[-1] != 128 or x.dtype != torch.float32 or not x.is_contiguous():
         raise ValueError("x must be contiguous float32 [B, S, 128]")
@@ -295,7 +298,7 @@ def fused_forward_d128(
     check(
         _launch("fused_forward_d128", lambda: lib().xb_fused_forward_d128(
             x.data_ptr(), out.data_ptr(), wpack.data_ptr(), ppack.data_ptr(), batch, seq_len,
-            num_heads, ffn_dim, num_layers, float(scale), stream_handle(x.device))),
+            num_heads, ffn_dim, num_layers, stream_handle(x.device))),
         "xb_fused_forward_d128",
     )
     return out

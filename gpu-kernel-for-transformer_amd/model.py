@@ -37,6 +37,8 @@ import torch.nn as nn
 from . import kernels
 from .config import ShapeExecutionPlan, TransformerConfig, resolve_shape_execution_plan
 
+_LOG2E = 1.4426950408889634
+
 
 class SelfAttentionParameters(nn.Module):
     """Parameter container with the reference's attention layout (TTB:207-220)."""
@@ -195,9 +197,13 @@ class UserOptimizedTransformer(nn.Module):
         with torch.no_grad():
             for layer in self.layers:
                 att = layer.attention
+                # softmax scale and log2(e) (the kernel exponentiates base 2) ride on Wq, bq
+                q_scale = att.scale * _LOG2E
                 for lin in (att.q_proj, att.k_proj, att.v_proj, att.out_proj, layer.ffn_in, layer.ffn_out):
-                    weights.append(kernels.pack_linear_fragments(lin.weight, natural=lin is att.out_proj))
-                for vec in (att.q_proj.bias, att.k_proj.bias, att.v_proj.bias, att.out_proj.bias,
+                    weights.append(kernels.pack_linear_fragments(
+                        lin.weight, natural=lin is att.out_proj, scale=q_scale if lin is att.q_proj else 1.0))
+                vectors.append(att.q_proj.bias.detach().float() * q_scale)
+                for vec in (att.k_proj.bias, att.v_proj.bias, att.out_proj.bias,
                             layer.ffn_in.bias, layer.ffn_out.bias, layer.norm1.weight, layer.norm1.bias,
                             layer.norm2.weight, layer.norm2.bias):
                     vectors.append(vec.detach().float().reshape(-1))
@@ -273,10 +279,7 @@ class UserOptimizedTransformer(nn.Module):
         cfg = self.config
         if self._uses_fused_stack(x):
             wpack, ppack = self._fused_stack_parameters()
-            return kernels.fused_forward_d128(
-                x, wpack, ppack, cfg.num_heads, cfg.ffn_dim, len(self.layers),
-                self.layers[0].attention.scale, out=out,
-            )
+            return kernels.fused_forward_d128(x, wpack, ppack, cfg.num_heads, cfg.ffn_dim, len(self.layers), out=out)
         batch, seq_len, d_model = x.shape
         rows = batch * seq_len
         dev = x.device

@@ -98,13 +98,14 @@ int xb_attention_causal(const void* qkv, void* out, int32_t batch,
 /*
  * Packs an FP32 nn.Linear weight w[n, k] (n % 16 == 0, k % 32 == 0) into the
  * FP16 fragment-major order xb_fused_forward_d128 streams its weights in:
- *   out[((ob * (k/32) + ks) * 64 + l) * 8 + m] = w[16*ob + l%16][k(ks, l, m)]
+ *   out[((ob * (k/32) + ks) * 64 + l) * 8 + m] = scale * w[16*ob + l%16][k(ks, l, m)]
  * with k(ks, l, m) given by `order` (one 16-byte MFMA operand per lane, 1 KiB
- * per 16x32 block).  Replaces the reference's cached weight conversions
+ * per 16x32 block); `scale` multiplies in FP32 before the FP16 rounding.
+ * Replaces the reference's cached weight conversions
  * (_cached_linear_parameters / _packed_qkv, torch_transformer_benchmark.py:540-641).
  */
 int xb_pack_linear_fragments(const float* w, void* out, int32_t n, int32_t k,
-                             int32_t order, void* stream);
+                             int32_t order, float scale, void* stream);
 
 /*
  * The whole forward (every layer and the final LayerNorm) for d_model == 128,
@@ -116,16 +117,18 @@ int xb_pack_linear_fragments(const float* w, void* out, int32_t n, int32_t k,
  *   wpack: per layer, fragment-packed (xb_pack_linear_fragments) Wq, Wk, Wv,
  *          Wo [128,128], W1 [ffn,128], W2 [128,ffn], layers back to back; Wo
  *          in XB_PACK_NATURAL order, the others in XB_PACK_PERMUTED order;
- *   ppack: FP32, per layer bq, bk, bv, bo [128], b1 [ffn], b2 [128],
- *          norm1 gamma, beta, norm2 gamma, beta [128 each]; then final_norm
- *          gamma, beta.
+ *          Wq packed with scale = softmax_scale * log2(e);
+ *   ppack: FP32, per layer bq * softmax_scale * log2(e), bk, bv, bo [128],
+ *          b1 [ffn], b2 [128], norm1 gamma, beta, norm2 gamma, beta [128
+ *          each]; then final_norm gamma, beta.
+ * (softmax_scale is head_dim ** -0.5, torch_transformer_benchmark.py:215.)
  * Replaces _forward_cuda_fused_norm (torch_transformer_benchmark.py:1092-1148)
  * for the official d_model = 128 shapes.
  */
 int xb_fused_forward_d128(const float* x, float* y, const void* wpack,
                           const float* ppack, int64_t batch, int32_t seq_len,
                           int32_t heads, int32_t ffn_dim, int32_t layers,
-                          float scale, void* stream);
+                          void* stream);
 
 #ifdef __cplusplus
 }

@@ -100,9 +100,9 @@ def test_pack_linear_fragments_layout(pkg, cuda):
     kernels = __import__(pkg.__name__ + ".kernels", fromlist=["pack_linear_fragments"])
     n, k = 48, 96
     w = torch.randn(n, k, generator=torch.Generator().manual_seed(2))
-    wh = w.half()
+    wh = (w * 0.75).half()
     for natural in (False, True):
-        packed = kernels.pack_linear_fragments(w.to(cuda), natural=natural).cpu()
+        packed = kernels.pack_linear_fragments(w.to(cuda), natural=natural, scale=0.75).cpu()
         expect = torch.empty(n * k, dtype=torch.float16)
         idx = 0
         for ob in range(n // 16):
