@@ -11,49 +11,65 @@
 //
 // Work decomposition: one 256-thread block = 4 waves handles BQ = 64*NQ
 // consecutive queries of one head; wave w owns queries [16*NQ*w, 16*NQ*(w+1)).
-// Keys are streamed in tiles of BKEYS through LDS.
+// K and V tiles of BKEYS keys are double buffered in LDS, both row-major: the
+// next tile's global loads are in flight while the current tile is consumed,
+// one barrier per tile.
 //
 // Scores are formed transposed, S^T = K . Q^T (MFMA M = keys, N = queries), so
 // that each lane's accumulator holds scores of ONE query (column l % 16) for
 // keys 16*jb + 4*(l/16) + i.  That is exactly the B-operand layout of the
 // second product O^T = V^T . P^T once the MFMA k index (l/16)*8 + m is mapped
 // to key 32*t + 4*(l/16) + (m & 3) + 16*(m >> 2): probabilities never leave
-// registers.  The matching A operand reads V transposed, so V tiles are stored
-// in LDS as Vt[hd][key].
+// registers.  The matching A operand (V^T rows, that key order) is read from
+// the row-major V tile with gfx950's transposing LDS read ds_read_b64_tr_b16:
+// within a 16-lane group, lane j's element i is element j%4 of the 8 bytes
+// lane 4i + j/4 addresses, so lane (g, j) addresses
+// V[32t + 4g + j/4][16hb + 4(j%4)].
 //
-// Softmax is online in FP32 and base 2 (scale * log2(e) folded into the
-// scores); the running max is shared by the 4 lanes that own one query via two
-// cross-lane max steps per tile, and the running sum stays per lane until the
-// end.  Only tiles that straddle the diagonal pay for the mask.
+// Softmax is online in FP32, base 2, with Q pre-multiplied by scale*log2(e).
+// The row sum comes out of the MFMA as one extra O^T block whose V^T rows are
+// all ones, and the running maximum is only moved (and O rescaled) when a
+// tile's maximum exceeds it by more than 8 (probabilities then stay <= 2^8,
+// exact enough in FP16); the decision is wave-uniform.  Only tiles that
+// straddle the diagonal pay for the mask.
 #include "common.h"
 #include "../../include/xblock.h"
 
 namespace xb {
 
-template <int HD>
+template <int HD, int NQ>
 struct AttnCfg {
-  static constexpr int NQ = HD >= 256 ? 1 : 2;        // 16-query blocks per wave
   static constexpr int BKEYS = HD >= 256 ? 32 : 64;   // keys per LDS tile
-  static constexpr int HDP = HD < 32 ? 32 : HD;       // reduction dim of S^T, padded
-  static constexpr int HDO = HD < 16 ? 16 : HD;       // rows of O^T, padded
+  static constexpr int HDP = HD < 32 ? 32 : HD;       // K columns incl. zero pad (S^T reduction)
+  static constexpr int HDV = HD < 16 ? 16 : HD;       // V columns incl. zero pad (O^T rows)
   static constexpr int QPW = 16 * NQ;                 // queries per wave
   static constexpr int BQ = 4 * QPW;                  // queries per block
   static constexpr int LDK = HDP + 8;                 // K tile row stride (halves)
-  static constexpr int LDV = BKEYS + 4;               // Vt tile row stride (halves)
+  static constexpr int LDV = HDV + 8;                 // V tile row stride (halves)
+  static constexpr int KSTEPS = HDP / 32, KB = BKEYS / 16, HB = HDV / 16, KT = BKEYS / 32;
+  static constexpr int CPK = HD / 8;                  // 16-byte chunks per key row
+  static constexpr int CH = (BKEYS * CPK + 255) / 256;  // chunks per thread per tile
 };
 
-template <int HD>
-__global__ __launch_bounds__(256) void attn_causal_kernel(
+typedef short short4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ half4_t lds_read_tr16(const half_t* p) {
+  const short4_t v =
+      __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t*)(p));
+  return __builtin_bit_cast(half4_t, v);
+}
+
+template <int HD, int NQ>
+__global__ __launch_bounds__(256, 2) void attn_causal_kernel(
     const half_t* __restrict__ qkv, half_t* __restrict__ out, int H, int S,
     int q_tiles, float scale_log2) {
-  using Cfg = AttnCfg<HD>;
-  constexpr int NQ = Cfg::NQ, BKEYS = Cfg::BKEYS, HDP = Cfg::HDP, HDO = Cfg::HDO;
-  constexpr int QPW = Cfg::QPW, BQ = Cfg::BQ, LDK = Cfg::LDK, LDV = Cfg::LDV;
-  constexpr int KSTEPS = HDP / 32, KB = BKEYS / 16, HB = HDO / 16;
-  constexpr int CPK = HD / 8;  // 16-byte chunks per key row
+  using C = AttnCfg<HD, NQ>;
+  constexpr int BKEYS = C::BKEYS, HDP = C::HDP, HDV = C::HDV, QPW = C::QPW, BQ = C::BQ;
+  constexpr int LDK = C::LDK, LDV = C::LDV, KSTEPS = C::KSTEPS, KB = C::KB, HB = C::HB;
+  constexpr int KT = C::KT, CPK = C::CPK, CH = C::CH;
 
-  __shared__ __attribute__((aligned(16))) half_t k_lds[BKEYS * LDK];
-  __shared__ __attribute__((aligned(16))) half_t v_lds[HDO * LDV];
+  __shared__ __attribute__((aligned(16))) half_t k_lds[2][BKEYS * LDK];
+  __shared__ __attribute__((aligned(16))) half_t v_lds[2][BKEYS * LDV];
 
   // Heaviest query tiles (most keys under the causal mask) are issued first.
   const int bh = blockIdx.x / q_tiles;
@@ -66,148 +82,188 @@ __global__ __launch_bounds__(256) void attn_causal_kernel(
   const half_t* vbase = base + 2 * D;
 
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int g = lane / 16, r16 = lane % 16;
   const int q0 = qt * BQ;
   const int qw0 = q0 + wave * QPW;
 
-  // Zero the padding columns/rows once; tile loads never touch them.
+  // Zero the padding columns of both buffers once; tile stores never touch them.
   if constexpr (HDP > HD) {
-    for (int i = tid; i < BKEYS * (HDP - HD); i += 256)
-      k_lds[(i / (HDP - HD)) * LDK + HD + i % (HDP - HD)] = (half_t)0.f;
+    for (int i = tid; i < 2 * BKEYS * (HDP - HD); i += 256) {
+      const int buf = i / (BKEYS * (HDP - HD)), j = i % (BKEYS * (HDP - HD));
+      k_lds[buf][(j / (HDP - HD)) * LDK + HD + j % (HDP - HD)] = (half_t)0.f;
+    }
   }
-  if constexpr (HDO > HD) {
-    for (int i = tid; i < (HDO - HD) * LDV; i += 256) v_lds[HD * LDV + i] = (half_t)0.f;
+  if constexpr (HDV > HD) {
+    for (int i = tid; i < 2 * BKEYS * (HDV - HD); i += 256) {
+      const int buf = i / (BKEYS * (HDV - HD)), j = i % (BKEYS * (HDV - HD));
+      v_lds[buf][(j / (HDV - HD)) * LDV + HD + j % (HDV - HD)] = (half_t)0.f;
+    }
   }
 
-  // Q fragments (B operand of S^T): lane holds q[query][32*ks + 8*(l/16) .. +7].
+  // Q fragments (B operand of S^T), pre-multiplied by scale * log2(e):
+  // lane holds q[query][32*ks + 8*(l/16) .. +7].
   half8_t qf[NQ][KSTEPS];
   const half8_t zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
   for (int qb = 0; qb < NQ; ++qb) {
-    const int q = qw0 + 16 * qb + lane % 16;
+    const int q = qw0 + 16 * qb + r16;
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) {
-      const int d = 32 * ks + 8 * (lane / 16);
-      qf[qb][ks] = (q < S && d < HD) ? *reinterpret_cast<const half8_t*>(base + q * row_stride + d) : zero8;
+      const int d = 32 * ks + 8 * g;
+      half8_t v = zero8;
+      if (q < S && d < HD) {
+        v = *reinterpret_cast<const half8_t*>(base + q * row_stride + d);
+#pragma unroll
+        for (int m = 0; m < 8; ++m) v[m] = (half_t)((float)v[m] * scale_log2);
+      }
+      qf[qb][ks] = v;
     }
   }
 
-  float4_t o[HB][NQ];
+  float4_t o[HB][NQ], lacc[NQ];
+  float m_run[NQ];
 #pragma unroll
-  for (int i = 0; i < HB; ++i)
+  for (int qb = 0; qb < NQ; ++qb) {
 #pragma unroll
-    for (int j = 0; j < NQ; ++j) o[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
-  float m_run[NQ], l_run[NQ];
+    for (int hb = 0; hb < HB; ++hb) o[hb][qb] = float4_t{0.f, 0.f, 0.f, 0.f};
+    lacc[qb] = float4_t{0.f, 0.f, 0.f, 0.f};
+    m_run[qb] = -INFINITY;
+  }
+  const half8_t ones8 = {1, 1, 1, 1, 1, 1, 1, 1};
+
+  half8_t kreg[CH], vreg[CH];
+  auto gload = [&](int k0) {
 #pragma unroll
-  for (int j = 0; j < NQ; ++j) { m_run[j] = -INFINITY; l_run[j] = 0.f; }
+    for (int j = 0; j < CH; ++j) {
+      const int id = tid + 256 * j;
+      kreg[j] = zero8;
+      vreg[j] = zero8;
+      if (id < BKEYS * CPK) {
+        const int key = k0 + id / CPK, c = (id % CPK) * 8;
+        if (key < S) {
+          kreg[j] = *reinterpret_cast<const half8_t*>(kbase + key * row_stride + c);
+          vreg[j] = *reinterpret_cast<const half8_t*>(vbase + key * row_stride + c);
+        }
+      }
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int id = tid + 256 * j;
+      if (id < BKEYS * CPK) {
+        const int r = id / CPK, c = (id % CPK) * 8;
+        *reinterpret_cast<half8_t*>(&k_lds[buf][r * LDK + c]) = kreg[j];
+        *reinterpret_cast<half8_t*>(&v_lds[buf][r * LDV + c]) = vreg[j];
+      }
+    }
+  };
 
   const int key_end = min(S, q0 + BQ);
   const int n_tiles = (key_end + BKEYS - 1) / BKEYS;
+  gload(0);
+  sstore(0);
+  __syncthreads();
   for (int t = 0; t < n_tiles; ++t) {
+    const int cur = t & 1;
     const int k0 = t * BKEYS;
-    __syncthreads();  // previous tile fully consumed
-    for (int id = tid; id < BKEYS * CPK; id += 256) {
-      const int r = id / CPK, c = (id % CPK) * 8;
-      const int key = k0 + r;
-      half8_t kv = zero8, vv = zero8;
-      if (key < S) {
-        kv = *reinterpret_cast<const half8_t*>(kbase + key * row_stride + c);
-        vv = *reinterpret_cast<const half8_t*>(vbase + key * row_stride + c);
-      }
-      *reinterpret_cast<half8_t*>(k_lds + r * LDK + c) = kv;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v_lds[(c + e) * LDV + r] = vv[e];
-    }
-    __syncthreads();
+    if (t + 1 < n_tiles) gload(k0 + BKEYS);
 
     // Wave-uniform skip: every key of this tile lies above this wave's diagonal.
-    if (k0 > qw0 + QPW - 1) continue;
-    const bool diag = (k0 + BKEYS - 1 > qw0);
+    if (k0 <= qw0 + QPW - 1) {
+      const bool diag = (k0 + BKEYS - 1 > qw0);
+      const half_t* kt_lds = k_lds[cur];
+      const half_t* vt_lds = v_lds[cur];
 
-    // S^T tile = K . Q^T  ->  s[jb][qb][i]: key k0+16jb+4(l/16)+i, query qw0+16qb+l%16
-    float4_t s[KB][NQ];
+      // S^T tile = K . Q^T  ->  s[jb][qb][i]: key k0+16jb+4g+i, query qw0+16qb+r16
+      float4_t s[KB][NQ];
 #pragma unroll
-    for (int jb = 0; jb < KB; ++jb) {
+      for (int jb = 0; jb < KB; ++jb) {
 #pragma unroll
-      for (int qb = 0; qb < NQ; ++qb) s[jb][qb] = float4_t{0.f, 0.f, 0.f, 0.f};
+        for (int qb = 0; qb < NQ; ++qb) s[jb][qb] = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < KSTEPS; ++ks) {
-        const half8_t kf = *reinterpret_cast<const half8_t*>(
-            k_lds + (16 * jb + lane % 16) * LDK + 32 * ks + 8 * (lane / 16));
+        for (int ks = 0; ks < KSTEPS; ++ks) {
+          const half8_t kf = *reinterpret_cast<const half8_t*>(kt_lds + (16 * jb + r16) * LDK + 32 * ks + 8 * g);
 #pragma unroll
-        for (int qb = 0; qb < NQ; ++qb) s[jb][qb] = mfma16x16x32(kf, qf[qb][ks], s[jb][qb]);
+          for (int qb = 0; qb < NQ; ++qb) s[jb][qb] = mfma16x16x32(kf, qf[qb][ks], s[jb][qb]);
+        }
+      }
+      if (diag) {
+#pragma unroll
+        for (int jb = 0; jb < KB; ++jb)
+#pragma unroll
+          for (int qb = 0; qb < NQ; ++qb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (k0 + 16 * jb + 4 * g + i > qw0 + 16 * qb + r16) s[jb][qb][i] = -INFINITY;
+      }
+
+      // Tile maximum per query; move the running maximum only when it grew by > 8.
+      float mx[NQ];
+      bool grow = false;
+#pragma unroll
+      for (int qb = 0; qb < NQ; ++qb) {
+        float m = -INFINITY;
+#pragma unroll
+        for (int jb = 0; jb < KB; ++jb)
+          m = fmaxf(m, fmaxf(fmaxf(s[jb][qb][0], s[jb][qb][1]), fmaxf(s[jb][qb][2], s[jb][qb][3])));
+        m = fmaxf(m, __shfl_xor(m, 16));
+        m = fmaxf(m, __shfl_xor(m, 32));
+        mx[qb] = m;
+        grow |= m > m_run[qb] + 8.0f;
+      }
+      if (__any(grow)) {
+#pragma unroll
+        for (int qb = 0; qb < NQ; ++qb) {
+          const float m_new = fmaxf(m_run[qb], mx[qb]);
+          const float corr = __builtin_amdgcn_exp2f(m_run[qb] - m_new);
+          m_run[qb] = m_new;
+#pragma unroll
+          for (int hb = 0; hb < HB; ++hb) o[hb][qb] *= corr;
+          lacc[qb] *= corr;
+        }
+      }
+
+      // O^T += V^T . P^T (and the row sums via an all-ones V^T block), 32 keys per step.
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) {
+        half8_t pf[NQ];
+#pragma unroll
+        for (int qb = 0; qb < NQ; ++qb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            pf[qb][i] = (half_t)__builtin_amdgcn_exp2f(s[2 * kt][qb][i] - m_run[qb]);
+            pf[qb][4 + i] = (half_t)__builtin_amdgcn_exp2f(s[2 * kt + 1][qb][i] - m_run[qb]);
+          }
+#pragma unroll
+        for (int qb = 0; qb < NQ; ++qb) lacc[qb] = mfma16x16x32(ones8, pf[qb], lacc[qb]);
+        const half_t* vrow = vt_lds + (32 * kt + 4 * g + r16 / 4) * LDV + 4 * (r16 % 4);
+#pragma unroll
+        for (int hb = 0; hb < HB; ++hb) {
+          const half4_t lo = lds_read_tr16(vrow + 16 * hb);
+          const half4_t hi = lds_read_tr16(vrow + 16 * LDV + 16 * hb);
+          const half8_t vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+          for (int qb = 0; qb < NQ; ++qb) o[hb][qb] = mfma16x16x32(vf, pf[qb], o[hb][qb]);
+        }
       }
     }
 
-#pragma unroll
-    for (int qb = 0; qb < NQ; ++qb) {
-      const int q = qw0 + 16 * qb + lane % 16;
-      float mx = -INFINITY;
-#pragma unroll
-      for (int jb = 0; jb < KB; ++jb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float v = s[jb][qb][i] * scale_log2;
-          if (diag && (k0 + 16 * jb + 4 * (lane / 16) + i > q)) v = -INFINITY;
-          s[jb][qb][i] = v;
-          mx = fmaxf(mx, v);
-        }
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m_run[qb], mx);
-      const float corr = __builtin_amdgcn_exp2f(m_run[qb] - m_new);
-      m_run[qb] = m_new;
-      float rs = 0.f;
-#pragma unroll
-      for (int jb = 0; jb < KB; ++jb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float p = __builtin_amdgcn_exp2f(s[jb][qb][i] - m_new);
-          s[jb][qb][i] = p;
-          rs += p;
-        }
-      l_run[qb] = l_run[qb] * corr + rs;
-#pragma unroll
-      for (int hb = 0; hb < HB; ++hb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) o[hb][qb][i] *= corr;
-    }
-
-    // O^T += V^T . P^T over 32-key steps.
-#pragma unroll
-    for (int ks = 0; ks < BKEYS / 32; ++ks) {
-      half8_t pf[NQ];
-#pragma unroll
-      for (int qb = 0; qb < NQ; ++qb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          pf[qb][i] = (half_t)s[2 * ks][qb][i];
-          pf[qb][4 + i] = (half_t)s[2 * ks + 1][qb][i];
-        }
-#pragma unroll
-      for (int hb = 0; hb < HB; ++hb) {
-        const half_t* vr = v_lds + (16 * hb + lane % 16) * LDV + 32 * ks + 4 * (lane / 16);
-        const half4_t lo = *reinterpret_cast<const half4_t*>(vr);
-        const half4_t hi = *reinterpret_cast<const half4_t*>(vr + 16);
-        const half8_t vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-#pragma unroll
-        for (int qb = 0; qb < NQ; ++qb) o[hb][qb] = mfma16x16x32(vf, pf[qb], o[hb][qb]);
-      }
-    }
+    if (t + 1 < n_tiles) sstore(cur ^ 1);
+    __syncthreads();
   }
 
-  // Normalise and store: lane holds O^T[16hb + 4(l/16) + i][query l%16].
+  // Normalise and store: lane holds O^T[16hb + 4g + i][query r16]; every row of
+  // the all-ones block holds that query's probability sum.
   half_t* obase = out + (int64_t)b * S * D + (int64_t)h * HD;
 #pragma unroll
   for (int qb = 0; qb < NQ; ++qb) {
-    float l = l_run[qb];
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
-    const float inv = 1.0f / l;
-    const int q = qw0 + 16 * qb + lane % 16;
+    const float inv = 1.0f / lacc[qb][0];
+    const int q = qw0 + 16 * qb + r16;
     if (q >= S) continue;
 #pragma unroll
     for (int hb = 0; hb < HB; ++hb) {
-      const int d = 16 * hb + 4 * (lane / 16);
+      const int d = 16 * hb + 4 * g;
       if (d < HD) {
         half4_t r;
 #pragma unroll
@@ -218,17 +274,32 @@ __global__ __launch_bounds__(256) void attn_causal_kernel(
   }
 }
 
-template <int HD>
+template <int HD, int NQ>
 static hipError_t launch_attn(const half_t* qkv, half_t* out, int B, int S, int H, float scale,
                               hipStream_t s) {
-  constexpr int BQ = AttnCfg<HD>::BQ;
+  constexpr int BQ = AttnCfg<HD, NQ>::BQ;
   const int q_tiles = (S + BQ - 1) / BQ;
   const int64_t blocks = (int64_t)q_tiles * B * H;
   if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
   const float scale_log2 = scale * 1.44269504088896340736f;
-  hipLaunchKernelGGL((attn_causal_kernel<HD>), dim3((unsigned)blocks), dim3(256), 0, s, qkv, out,
+  hipLaunchKernelGGL((attn_causal_kernel<HD, NQ>), dim3((unsigned)blocks), dim3(256), 0, s, qkv, out,
                      H, S, q_tiles, scale_log2);
   return hipGetLastError();
+}
+
+// Long sequences take 64 queries per wave (each K/V fragment read from LDS
+// then feeds 4 MFMAs); short ones keep 32 so a block does not outgrow S.
+template <int HD>
+static hipError_t dispatch_attn(const half_t* qkv, half_t* out, int B, int S, int H, float scale,
+                                hipStream_t s) {
+  if constexpr (HD >= 256) {
+    return launch_attn<HD, 1>(qkv, out, B, S, H, scale, s);
+  } else if constexpr (HD >= 128) {
+    return launch_attn<HD, 2>(qkv, out, B, S, H, scale, s);
+  } else {
+    if (S >= 1024) return launch_attn<HD, 4>(qkv, out, B, S, H, scale, s);
+    return launch_attn<HD, 2>(qkv, out, B, S, H, scale, s);
+  }
 }
 
 }  // namespace xb
@@ -251,13 +322,12 @@ extern "C" int xb_attention_causal(const void* qkv, void* out, int32_t batch, in
   const int S = (int)seq_len;
   hipError_t e;
   switch (head_dim) {
-    case 8: e = launch_attn<8>(q, o, batch, S, heads, scale, s); break;
-    case 16: e = launch_attn<16>(q, o, batch, S, heads, scale, s); break;
-    case 32: e = launch_attn<32>(q, o, batch, S, heads, scale, s); break;
-    case 64: e = launch_attn<64>(q, o, batch, S, heads, scale, s); break;
-    case 128: e = launch_attn<128>(q, o, batch, S, heads, scale, s); break;
-    case 256: e = launch_attn<256>(q, o, batch, S, heads, scale, s); break;
-    default: return XB_ERR_UNSUPPORTED_SHAPE;
+    case 8: e = dispatch_attn<8>(q, o, batch, S, heads, scale, s); break;
+    case 16: e = dispatch_attn<16>(q, o, batch, S, heads, scale, s); break;
+    case 32: e = dispatch_attn<32>(q, o, batch, S, heads, scale, s); break;
+    case 64: e = dispatch_attn<64>(q, o, batch, S, heads, scale, s); break;
+    case 128: e = dispatch_attn<128>(q, o, batch, S, heads, scale, s); break;
+    default: e = dispatch_attn<256>(q, o, batch, S, heads, scale, s); break;
   }
   return (int)e;
 }
