@@ -42,10 +42,13 @@ def _hipcc() -> str:
 
 # Per-file additions.  The attention kernels mask with -inf and never see
 # NaN, so they drop IEEE NaN handling: max/min then compile to a single
-# v_max/v_min instead of a canonicalising pair.
+# v_max/v_min instead of a canonicalising pair.  The GEMM keeps its MFMA
+# accumulators in VGPRs: the AGPR form makes the register allocator copy
+# accumulator tuples around the K loop.
 EXTRA_FLAGS = {
     "fused_d128.hip": ["-fno-honor-nans"],
     "attention.hip": ["-fno-honor-nans"],
+    "gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

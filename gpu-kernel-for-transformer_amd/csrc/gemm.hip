@@ -9,11 +9,16 @@
 // computes GELU with tanh (triton_fused_ffn.py:198-213); the baseline it must
 // match uses exact erf (torch_transformer_benchmark.py:286), as done here.
 //
-// Block = 4 waves in a 2 x 2 grid; each wave owns a (BM/2) x (BN/2) sub-tile.
-// Tiles of A and W go global -> registers -> padded LDS, double buffered, so
-// the next K-slab's global loads are in flight while MFMAs consume the
-// current one.  The epilogue stages the FP16 tile through LDS so the stores
-// to C are full 16-byte row segments.
+// Two kernels:
+//  * gemm_dma_kernel (K % 64 == 0, K >= 256): 8 waves, up to 256 x 256 tiles,
+//    direct global -> LDS loads; used for the D >= 256 projections and FFN.
+//  * gemm_nt_kernel (any K % 8 == 0): 4 waves in a 2 x 2 grid, tiles of A and
+//    W go global -> registers -> padded LDS, double buffered; the epilogue
+//    stages the FP16 tile through LDS so the stores to C are full 16-byte row
+//    segments.
+// Accumulators stay in VGPRs (the library builds this file with
+// -amdgpu-mfma-vgpr-form): with AGPR accumulators the register allocator
+// rotates accumulator tuples through copies on every loop iteration.
 #include "common.h"
 #include "../../include/xblock.h"
 
@@ -30,17 +35,18 @@ __device__ __forceinline__ int xcd_contiguous_tile(int b, int nb) {
   return x * q + (x < r ? x : r) + b / 8;
 }
 
-template <int BM, int BN, int EPI>
-__global__ __launch_bounds__(256, 2) void gemm_nt_kernel(
+template <int BM, int BN, int WGM, int WGN, int EPI>
+__global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_nt_kernel(
     const half_t* __restrict__ A, const half_t* __restrict__ W,
     const float* __restrict__ bias, half_t* __restrict__ C, int M, int N,
     int K, int tiles_n) {
+  constexpr int NT = 64 * WGM * WGN;  // threads
   constexpr int BK = kGemmBK, LDK = kGemmLDK;
-  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int WM = BM / WGM, WN = BN / WGN;  // wave tile
   constexpr int FM = WM / 16, FN = WN / 16;
   constexpr int CPR = BK / 8;  // 16-byte chunks per tile row
-  constexpr int A_CH = BM * CPR / 256, B_CH = BN * CPR / 256;
-  static_assert(A_CH * 256 == BM * CPR && B_CH * 256 == BN * CPR, "tile/thread mismatch");
+  constexpr int A_CH = BM * CPR / NT, B_CH = BN * CPR / NT;
+  static_assert(A_CH * NT == BM * CPR && B_CH * NT == BN * CPR, "tile/thread mismatch");
   constexpr int LDC = BN + 8;
   static_assert(BM * LDC <= 2 * (BM + BN) * LDK, "epilogue staging must fit");
   __shared__ __attribute__((aligned(16))) half_t smem[2 * (BM + BN) * LDK];
@@ -48,20 +54,20 @@ __global__ __launch_bounds__(256, 2) void gemm_nt_kernel(
   const int tile = xcd_contiguous_tile(blockIdx.x, gridDim.x);
   const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
-  const int wm = (wave / 2) * WM, wn = (wave % 2) * WN;
+  const int wm = (wave / WGN) * WM, wn = (wave % WGN) * WN;
 
   half8_t ra[A_CH], rb[B_CH];
   const half8_t zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
   auto gload = [&](int k0) {
 #pragma unroll
     for (int j = 0; j < A_CH; ++j) {
-      const int id = tid + 256 * j, r = id / CPR, c = id % CPR;
+      const int id = tid + NT * j, r = id / CPR, c = id % CPR;
       const int gm = m0 + r, gk = k0 + c * 8;
       ra[j] = (gm < M && gk < K) ? *reinterpret_cast<const half8_t*>(A + (int64_t)gm * K + gk) : zero8;
     }
 #pragma unroll
     for (int j = 0; j < B_CH; ++j) {
-      const int id = tid + 256 * j, r = id / CPR, c = id % CPR;
+      const int id = tid + NT * j, r = id / CPR, c = id % CPR;
       const int gn = n0 + r, gk = k0 + c * 8;
       rb[j] = (gn < N && gk < K) ? *reinterpret_cast<const half8_t*>(W + (int64_t)gn * K + gk) : zero8;
     }
@@ -71,12 +77,12 @@ __global__ __launch_bounds__(256, 2) void gemm_nt_kernel(
     half_t* bs = as + BM * LDK;
 #pragma unroll
     for (int j = 0; j < A_CH; ++j) {
-      const int id = tid + 256 * j;
+      const int id = tid + NT * j;
       *reinterpret_cast<half8_t*>(as + (id / CPR) * LDK + (id % CPR) * 8) = ra[j];
     }
 #pragma unroll
     for (int j = 0; j < B_CH; ++j) {
-      const int id = tid + 256 * j;
+      const int id = tid + NT * j;
       *reinterpret_cast<half8_t*>(bs + (id / CPR) * LDK + (id % CPR) * 8) = rb[j];
     }
   };
@@ -131,33 +137,194 @@ __global__ __launch_bounds__(256, 2) void gemm_nt_kernel(
       }
   }
   __syncthreads();
-  constexpr int CCH = BM * (BN / 8) / 256;
+  constexpr int CCH = BM * (BN / 8) / NT;
 #pragma unroll
   for (int j = 0; j < CCH; ++j) {
-    const int id = tid + 256 * j, r = id / (BN / 8), c = (id % (BN / 8)) * 8;
+    const int id = tid + NT * j, r = id / (BN / 8), c = (id % (BN / 8)) * 8;
     const int gm = m0 + r, gn = n0 + c;
     if (gm < M && gn < N)
       *reinterpret_cast<half8_t*>(C + (int64_t)gm * N + gn) = *reinterpret_cast<const half8_t*>(cs + r * LDC + c);
   }
 }
 
-template <int BM, int BN, int EPI>
+// ---------------------------------------------------------------------------
+// Large-tile kernel for K % 64 == 0.  8 waves (2 per SIMD) share a BM x BN
+// tile; each wave owns a (BM/WGM) x (BN/WGN) sub-tile with its FP32
+// accumulators in VGPRs.  Operands reach LDS by direct global -> LDS loads
+// (global_load_lds_dwordx4), one 64-wide K slab at a time, double buffered:
+// slab kt+2 is requested as soon as every wave has read slab kt.
+//
+// LDS slab layout: the A rows (BM) and then the W rows (BN), 128 bytes each
+// (64 halves = eight 16-byte chunks).  Chunk c of row r lives at slot
+// c ^ (r & 7), so the 8 rows one 8-lane phase of ds_read_b128 touches land in
+// 8 distinct 16-byte bank groups.  A DMA load writes lane i's 16 bytes to
+// consecutive LDS addresses, so the swizzle is applied on the global side:
+// lane i of a 1 KB segment (8 rows) fetches the chunk that belongs in its slot.
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void global_void_t;
+
+
+// s_waitcnt with vmcnt <= N and lgkmcnt == 0 (gfx9 field layout:
+// vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt_hi[15:14]).
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | ((N >> 4) << 14));
+}
+
+// Workgroup barrier that orders this wave's memory operations in the compiler
+// without the vmcnt(0) a release fence would add.
+__device__ __forceinline__ void slab_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ int row128_offset(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
+
+template <int BM, int BN, int WGM, int WGN, int EPI>
+__global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_kernel(
+    const half_t* __restrict__ A, const half_t* __restrict__ W,
+    const float* __restrict__ bias, half_t* __restrict__ C, int M, int N,
+    int K, int tiles_n) {
+  constexpr int NW = WGM * WGN;
+  constexpr int WM = BM / WGM, WN = BN / WGN, FM = WM / 16, FN = WN / 16;
+  constexpr int SLAB = (BM + BN) * 128;        // 64-wide K slab, 128-byte rows
+  constexpr int SEGS = (BM + BN) / 8;          // 1 KB wave-loads per slab (8 rows)
+  constexpr int SPW = SEGS / NW;
+  static_assert(SEGS % NW == 0 && WM % 16 == 0 && WN % 16 == 0, "tile shape");
+  __shared__ __attribute__((aligned(1024))) char smem[2 * SLAB];
+  const int tile = xcd_contiguous_tile(blockIdx.x, gridDim.x);
+  const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
+  const int lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int wm = (wave / WGN) * WM, wn = (wave % WGN) * WN;
+  const half_t* src[SPW];
+#pragma unroll
+  for (int j = 0; j < SPW; ++j) {
+    const int r = (wave + NW * j) * 8 + lane / 8;
+    const int c = (lane % 8) ^ (r & 7);
+    src[j] = r < BM ? A + (int64_t)min(m0 + r, M - 1) * K + 8 * c
+                    : W + (int64_t)min(n0 + r - BM, N - 1) * K + 8 * c;
+  }
+  auto issue = [&](int kt, int stage) {
+#pragma unroll
+    for (int j = 0; j < SPW; ++j)
+      __builtin_amdgcn_global_load_lds((global_void_t*)(src[j] + kt * 64),
+                                       (lds_void_t*)(smem + stage * SLAB + (wave + NW * j) * 1024), 16, 0, 0);
+  };
+  float4_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+  const int KT = K / 64;
+  auto read_frags = [&](int kt, int ks, half8_t (&af)[FM], half8_t (&bf)[FN]) {
+    const char* st = smem + (kt & 1) * SLAB;
+    const int q = ks * 4 + lane / 16;
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+      bf[j] = *reinterpret_cast<const half8_t*>(st + row128_offset(BM + wn + 16 * j + lane % 16, q));
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+      af[i] = *reinterpret_cast<const half8_t*>(st + row128_offset(wm + 16 * i + lane % 16, q));
+  };
+  auto mma = [&](const half8_t (&af)[FM], const half8_t (&bf)[FN]) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[i][j] = mfma16x16x32(bf[j], af[i], acc[i][j]);
+  };
+  // Slab kt: sub-step 0 reads sub-step 1's fragments of the same slab while
+  // its own MFMAs run; sub-step 1 waits for slab kt+1, refills slab kt's stage
+  // with slab kt+2 and reads slab kt+1's first fragments.
+  half8_t a0[FM], b0[FN], a1[FM], b1[FN];
+  issue(0, 0);
+  if (KT > 1) issue(1, 1);
+  if (KT > 1) wait_vm_lgkm0<SPW>(); else wait_vm_lgkm0<0>();
+  slab_barrier();
+  read_frags(0, 0, a0, b0);
+  for (int kt = 0; kt < KT; ++kt) {
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(kt, 1, a1, b1);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(a0, b0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (kt + 1 < KT) {
+      wait_vm_lgkm0<0>();
+      slab_barrier();
+      if (kt + 2 < KT) issue(kt + 2, kt & 1);
+      read_frags(kt + 1, 0, a0, b0);
+    } else {
+      wait_vm_lgkm0<0>();
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    mma(a1, b1);
+  }
+
+  // Epilogue: lane owns C[m][n .. n+3] for each (i, j); bias (+ GELU) in FP32
+  // and one 8-byte store per fragment.
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int n = n0 + wn + 16 * j + (lane / 16) * 4;
+    if (n >= N) continue;  // N % 8 == 0: n < N implies n + 3 < N
+    float b[4] = {0.f, 0.f, 0.f, 0.f};
+    if (bias != nullptr) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) b[e] = bias[n + e];
+    }
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int m = m0 + wm + 16 * i + lane % 16;
+      if (m >= M) continue;
+      half4_t h;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float v = acc[i][j][e] + b[e];
+        if constexpr (EPI == XB_EPI_BIAS_GELU) v = gelu_erf(v);
+        h[e] = (half_t)v;
+      }
+      *reinterpret_cast<half4_t*>(C + (int64_t)m * N + n) = h;
+    }
+  }
+}
+
+template <int BM, int BN, int WGM, int WGN, int EPI>
+static hipError_t launch_gemm_dma(const half_t* a, const half_t* w, const float* bias, half_t* c,
+                                  int64_t m, int n, int k, hipStream_t s) {
+  const int64_t tm = (m + BM - 1) / BM, tn = (n + BN - 1) / BN;
+  if (tm * tn > 0x7fffffffLL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, WGM, WGN, EPI>), dim3((unsigned)(tm * tn)),
+                     dim3(64 * WGM * WGN), 0, s, a, w, bias, c, (int)m, n, k, (int)tn);
+  return hipGetLastError();
+}
+
+template <int BM, int BN, int WGM, int WGN, int EPI>
 static hipError_t launch_gemm(const half_t* a, const half_t* w, const float* bias, half_t* c,
                               int64_t m, int n, int k, hipStream_t s) {
   const int64_t tm = (m + BM - 1) / BM, tn = (n + BN - 1) / BN;
   if (tm * tn > 0x7fffffffLL) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, EPI>), dim3((unsigned)(tm * tn)), dim3(256), 0, s,
-                     a, w, bias, c, (int)m, n, k, (int)tn);
+  hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, WGM, WGN, EPI>), dim3((unsigned)(tm * tn)),
+                     dim3(64 * WGM * WGN), 0, s, a, w, bias, c, (int)m, n, k, (int)tn);
   return hipGetLastError();
 }
 
 template <int EPI>
 static hipError_t dispatch_gemm(const half_t* a, const half_t* w, const float* bias, half_t* c,
                                 int64_t m, int n, int k, hipStream_t s) {
-  // Large tiles when they still give every CU a few tiles, else 64 x 64.
-  const int64_t big_tiles = ((m + 127) / 128) * ((n + 127) / 128);
-  if (big_tiles >= 512) return launch_gemm<128, 128, EPI>(a, w, bias, c, m, n, k, s);
-  return launch_gemm<64, 64, EPI>(a, w, bias, c, m, n, k, s);
+  auto tiles = [&](int64_t bm, int64_t bn) { return ((m + bm - 1) / bm) * ((n + bn - 1) / bn); };
+  if (k % 64 == 0 && k >= 256) {
+    // One block per CU: cost ~ rounds of 256 tiles x tile area, with the
+    // 256 x 256 tile ~15% cheaper per output (fewer LDS bytes per MFMA).
+    const int64_t big = (tiles(256, 256) + 255) / 256 * 65536 * 85 / 100;
+    const int64_t mid = (tiles(128, 256) + 255) / 256 * 32768;
+    const int64_t small = (tiles(128, 128) + 255) / 256 * 16384 * 115 / 100;
+    if (big <= mid && big <= small) return launch_gemm_dma<256, 256, 4, 2, EPI>(a, w, bias, c, m, n, k, s);
+    if (mid <= small) return launch_gemm_dma<128, 256, 2, 4, EPI>(a, w, bias, c, m, n, k, s);
+    return launch_gemm_dma<128, 128, 2, 2, EPI>(a, w, bias, c, m, n, k, s);
+  }
+  if (tiles(128, 128) >= 512) return launch_gemm<128, 128, 2, 2, EPI>(a, w, bias, c, m, n, k, s);
+  return launch_gemm<64, 64, 2, 2, EPI>(a, w, bias, c, m, n, k, s);
 }
 
 }  // namespace xb

@@ -80,7 +80,9 @@ def test_layer_norm_errors(pkg, cuda):
 @pytest.mark.parametrize(
     "m,n,k",
     [(1, 128, 128), (7, 384, 128), (8192, 384, 128), (8192, 128, 128), (1000, 1024, 1024),
-     (8192, 3072, 1024), (257, 136, 72), (64, 8, 8), (300, 1024, 128), (131072, 384, 128)],
+     (8192, 3072, 1024), (257, 136, 72), (64, 8, 8), (300, 1024, 128), (131072, 384, 128),
+     (8192, 4096, 256), (16000, 2056, 200), (33000, 1024, 136), (3000, 1032, 512),
+     (70000, 264, 1024)],
 )
 @pytest.mark.parametrize("gelu", [False, True])
 def test_linear(pkg, cuda, m, n, k, gelu):
