@@ -48,6 +48,9 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="bound on the CPU baseline's timed work")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--profile-only", action="store_true", help="only the headline timed steps (for rocprofv3)")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="with --profile-only: also run a plain 1 GiB elementwise copy (HBM counter calibration)")
+    p.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 FETCH_SIZE/WRITE_SIZE runs")
     return p.parse_args()
 
 
@@ -84,6 +87,64 @@ def roofline_of(bytes_, flops, seconds):
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+# Kernel symbol substring of each LaunchRecorder name (for counter CSVs).
+KERNEL_SYMBOLS = (("fused_forward_d128", "fused_stack_kernel"), ("attention", "attn_causal_kernel"),
+                  ("gemm_", "gemm_"), ("residual_layernorm", "ln_"), ("layernorm", "ln_"))
+CALIBRATION_BYTES = 1 << 30
+
+
+def measure_traffic(workload: int, dominant: str):
+    """HBM bytes per launch of `dominant` from two rocprofv3 --pmc runs of this script.
+
+    Each run (FETCH_SIZE, then WRITE_SIZE) replays the headline workload with
+    --profile-only plus a plain elementwise copy of CALIBRATION_BYTES; each
+    counter is scaled by what it reads for that copy (expected: exactly
+    CALIBRATION_BYTES read and written).  Returns (traffic_bytes, detail) or
+    (None, reason).
+    """
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+
+    prof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not Path(prof).exists():
+        return None, "rocprofv3 not found"
+    symbol = next((sym for prefix, sym in KERNEL_SYMBOLS if dominant.startswith(prefix)), None)
+    if symbol is None:
+        return None, f"no kernel symbol for {dominant}"
+    detail = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        out_dir = tempfile.mkdtemp(prefix=f"xb_{counter.lower()}_", dir="/tmp")
+        cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", out_dir, "-o", "run", "--",
+               sys.executable, str(REPO / "bench.py"), "--profile-only", "--copy-calibration",
+               "--workload", str(workload), "--steps", "2", "--warmup", "1"]
+        try:
+            proc = subprocess.run(cmd, cwd="/tmp", capture_output=True, text=True, timeout=240)
+        except subprocess.TimeoutExpired:
+            return None, f"rocprofv3 --pmc {counter} timed out"
+        files = list(Path(out_dir).rglob("*counter_collection.csv"))
+        if proc.returncode != 0 or not files:
+            return None, f"rocprofv3 --pmc {counter} failed (rc {proc.returncode})"
+        kernel_vals, copy_vals = [], []
+        for row in csv.DictReader(open(files[0])):
+            if row.get("Counter_Name") != counter:
+                continue
+            name, val = row["Kernel_Name"], float(row["Counter_Value"]) * 1024.0  # KiB -> bytes
+            if symbol in name:
+                kernel_vals.append(val)
+            elif "elementwise" in name:
+                copy_vals.append(val)
+        shutil.rmtree(out_dir, ignore_errors=True)
+        if not kernel_vals or not copy_vals or max(copy_vals) <= 0:
+            return None, f"{counter}: kernel or calibration dispatch missing"
+        factor = CALIBRATION_BYTES / max(copy_vals)
+        detail[counter] = {"raw_bytes": statistics.median(kernel_vals), "calibration_factor": factor,
+                           "bytes": statistics.median(kernel_vals) * factor, "dispatches": len(kernel_vals)}
+    total = detail["FETCH_SIZE"]["bytes"] + detail["WRITE_SIZE"]["bytes"]
+    return total, detail
 
 
 def main() -> int:
@@ -237,6 +298,16 @@ def main() -> int:
         del baseline, model, x, out
         torch.cuda.empty_cache()
 
+    if args.profile_only and args.copy_calibration:
+        # A plain streaming copy of known size: reads and writes exactly
+        # CALIBRATION_BYTES (the HBM counters' scale reference).
+        src = torch.ones(CALIBRATION_BYTES // 4, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.mul(src, 1.0, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
+
     cfg = headline["config"]
     line = {
         "metric": "tokens/sec per config on 1 MI355X; % of FP16 MFMA / HBM roofline",
@@ -267,6 +338,15 @@ def main() -> int:
         }
         line["kernels"] = {n: {"avg_us": round(v["avg_ms"] * 1e3, 2), "per_step": v["launches_per_step"],
                                "frac": round(v["frac"], 4), "bound": v["bound"]} for n, v in headline["kernels"].items()}
+    if "dominant" in headline and not args.no_traffic:
+        log(f"[bench] HBM traffic of {headline['dominant']}: two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE)")
+        traffic, detail = measure_traffic(args.workload, headline["dominant"])
+        line["roofline"]["traffic"] = traffic
+        line["roofline"]["traffic_detail"] = detail
+        if traffic is not None:
+            log(f"[bench] traffic {traffic / 1e9:.4f} GB per launch vs algorithmic {line['roofline']['bytes_per_launch'] / 1e9:.4f} GB")
+        else:
+            log(f"[bench] traffic unavailable: {detail}")
     if "cpu_baseline" in headline:
         line["cpu_baseline"] = headline["cpu_baseline"]
         line["accuracy"] = headline["accuracy"]
