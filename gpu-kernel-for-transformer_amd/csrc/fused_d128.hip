@@ -9,8 +9,11 @@
 //   ... ; y = LN_final(x)
 // with FP16 MFMA operands, FP32 accumulation, FP32 residual and softmax.
 //
-// Layout.  Wave w (of 4) owns token blocks w and 7-w (16 tokens each; the
-// pairing balances the causal attention work).  The residual stream stays in
+// Layout.  Eight waves (two per SIMD) each own one 16-token block: wave w
+// holds block w for w < 4 and block 11-w otherwise, so the two waves sharing
+// a SIMD (w and w+4) hold blocks b and 7-b and every SIMD gets the same causal
+// attention work.  (FUSED_WAVES=4 builds the one-wave-per-SIMD variant: wave w
+// owns blocks w and 7-w.)  The residual stream stays in
 // registers in the C layout of a "swapped" MFMA product out^T = W . act^T:
 // lane l holds token l%16 and features 16*fb + 4*(l/16) + i.  Read back as an
 // MFMA operand, that layout gives a k-step ks the reduction indices
@@ -75,11 +78,12 @@ __device__ __forceinline__ void row_stats(const float4_t (&r)[FB], float& mean, 
   rstd = rsqrtf(q * (1.0f / D) + 1e-5f);
 }
 
-// LayerNorm of the two register-resident token blocks -> MFMA operands.
-__device__ __forceinline__ void layer_norm(const float4_t (&res)[2][FB], const float* __restrict__ gamma,
-                                           const float* __restrict__ beta, half8_t (&xn)[2][KS], int g) {
+// LayerNorm of the wave's register-resident token blocks -> MFMA operands.
+template <int T>
+__device__ __forceinline__ void layer_norm(const float4_t (&res)[T][FB], const float* __restrict__ gamma,
+                                           const float* __restrict__ beta, half8_t (&xn)[T][KS], int g) {
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
+  for (int t = 0; t < T; ++t) {
     float mean, rstd;
     row_stats(res[t], mean, rstd);
 #pragma unroll
@@ -97,10 +101,19 @@ __device__ __forceinline__ void layer_norm(const float4_t (&res)[2][FB], const f
   }
 }
 
-// Weight fragments stream from L2 with PF output blocks in flight: one wave
-// per SIMD has no other wave to hide a load's latency behind, so the loads for
-// block ob + PF are issued before block ob's MFMAs.
-constexpr int PF = 4;
+// Waves per workgroup: 8 (two per SIMD, one 16-token block each) or 4 (one
+// per SIMD, two token blocks each).
+#ifndef FUSED_WAVES
+#define FUSED_WAVES 8
+#endif
+
+// Weight fragments stream from L2 with PF output blocks in flight: the loads
+// for block ob + PF are issued before block ob's MFMAs.  With one wave per
+// SIMD nothing else hides their latency, so that layout prefetches deeper.
+#ifndef FUSED_PF
+#define FUSED_PF (FUSED_WAVES == 8 ? 2 : 4)
+#endif
+constexpr int PF = FUSED_PF;
 
 // Fragments of output blocks [0, PF) of a weight with KIN k-steps.
 template <int KIN>
@@ -113,9 +126,9 @@ __device__ __forceinline__ void prefetch_head(const half_t* __restrict__ w, half
 
 // res[t][ob] += (W . act^T)[ob] + bias over all FB output blocks; `buf` holds
 // the fragments of blocks 0..PF-1 on entry (prefetch_head).
-template <int KIN>
+template <int KIN, int T>
 __device__ __forceinline__ void gemm_accumulate(const half_t* __restrict__ w, const float* __restrict__ bias,
-                                                const half8_t (&act)[2][KIN], float4_t (&res)[2][FB],
+                                                const half8_t (&act)[T][KIN], float4_t (&res)[T][FB],
                                                 half8_t (&buf)[PF][KIN], int lane, int g) {
 #pragma unroll
   for (int ob = 0; ob < FB; ++ob) {
@@ -126,23 +139,25 @@ __device__ __forceinline__ void gemm_accumulate(const half_t* __restrict__ w, co
 #pragma unroll
       for (int ks = 0; ks < KIN; ++ks) buf[ob % PF][ks] = frag(w, (ob + PF) * KIN + ks, lane);
     }
-    float4_t a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
+    float4_t a[T];
 #pragma unroll
-    for (int ks = 0; ks < KIN; ++ks) {
-      a0 = mfma16x16x32(cur[ks], act[0][ks], a0);
-      a1 = mfma16x16x32(cur[ks], act[1][ks], a1);
-    }
+    for (int t = 0; t < T; ++t) a[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KIN; ++ks)
+#pragma unroll
+      for (int t = 0; t < T; ++t) a[t] = mfma16x16x32(cur[ks], act[t][ks], a[t]);
     const float4_t b = ld4(bias + 16 * ob + 4 * g);
-    res[0][ob] += a0 + b;
-    res[1][ob] += a1 + b;
+#pragma unroll
+    for (int t = 0; t < T; ++t) res[t][ob] += a[t] + b;
   }
 }
 
-template <int HD>
-__global__ __launch_bounds__(256, 1) void fused_stack_kernel(
+template <int HD, int NW>
+__global__ __launch_bounds__(64 * NW, 1) void fused_stack_kernel(
     const float* __restrict__ x, float* __restrict__ y, const half_t* __restrict__ wpack,
     const float* __restrict__ ppack, int S, int layers) {
   constexpr int F = 128;  // ffn_dim (the packed-layer strides below assume it)
+  constexpr int T = 8 / NW;  // 16-token blocks per wave
   constexpr int H = D / HD;
   constexpr int FKS = F / 32;
   constexpr int HDB = HD < 16 ? 1 : HD / 16;   // 16-row blocks of one head in V^T / ctx
@@ -155,7 +170,10 @@ __global__ __launch_bounds__(256, 1) void fused_stack_kernel(
 
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int g = lane / 16, r16 = lane % 16;
-  const int tb0 = wave, tb1 = 7 - wave;
+  // Token block of the wave's t-th block.  Four waves: w and 7-w.  Eight waves
+  // (two per SIMD, waves w and w+4 sharing one): w for w < 4, else 11-w, so
+  // every SIMD again holds blocks b and 7-b.
+  auto tblock = [&](int t) { return NW == 4 ? (t ? 7 - wave : wave) : (wave < 4 ? wave : 11 - wave); };
   // Additive causal mask of a diagonal 16x16 block: key 4g + i vs query r16.
   float4_t diag_mask;
 #pragma unroll
@@ -165,10 +183,10 @@ __global__ __launch_bounds__(256, 1) void fused_stack_kernel(
   float* ys = y + seq * S * D;
 
   // Residual stream, C layout: res[t][fb][i] = x[16 tb_t + r16][16 fb + 4 g + i].
-  float4_t res[2][FB];
+  float4_t res[T][FB];
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int tok = 16 * (t ? tb1 : tb0) + r16;
+  for (int t = 0; t < T; ++t) {
+    const int tok = 16 * tblock(t) + r16;
 #pragma unroll
     for (int fb = 0; fb < FB; ++fb)
       res[t][fb] = tok < S ? ld4(xs + (int64_t)tok * D + 16 * fb + 4 * g) : float4_t{0.f, 0.f, 0.f, 0.f};
@@ -190,7 +208,7 @@ __global__ __launch_bounds__(256, 1) void fused_stack_kernel(
     const float* be2 = pp + 8 * D + F;
 
     // ---- LN1 and the QKV projection into LDS ------------------------------
-    half8_t xn[2][KS];
+    half8_t xn[T][KS];
     layer_norm(res, g1, be1, xn, g);
     __syncthreads();  // the previous layer's attention has finished reading K / V^T
     {
@@ -219,29 +237,33 @@ __global__ __launch_bounds__(256, 1) void fused_stack_kernel(
           // Q / K: swapped product, lane = (token r16, features 16fb + 4g + i).
           // Q's weights and bias arrive pre-multiplied by scale * log2(e).
           const float4_t b = ld4(bqkv + 16 * ob + 4 * g);
-          float4_t a0 = b, a1 = b;
+          float4_t a[T];
 #pragma unroll
-          for (int ks = 0; ks < KS; ++ks) {
-            a0 = mfma16x16x32(cur[ks], xn[0][ks], a0);
-            a1 = mfma16x16x32(cur[ks], xn[1][ks], a1);
-          }
+          for (int t = 0; t < T; ++t) a[t] = b;
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int t = 0; t < T; ++t) a[t] = mfma16x16x32(cur[ks], xn[t][ks], a[t]);
           const int fb = ob % FB;
           half_t* dst = ob < FB ? q_lds : k_lds;
-          *reinterpret_cast<half4_t*>(dst + (16 * tb0 + r16) * LD + 16 * fb + 4 * g) = to_half4(a0);
-          *reinterpret_cast<half4_t*>(dst + (16 * tb1 + r16) * LD + 16 * fb + 4 * g) = to_half4(a1);
+#pragma unroll
+          for (int t = 0; t < T; ++t)
+            *reinterpret_cast<half4_t*>(dst + (16 * tblock(t) + r16) * LD + 16 * fb + 4 * g) = to_half4(a[t]);
         } else {
           // V: unswapped product, lane = (tokens 16tb + 4g + i, feature 16fb + r16),
           // i.e. four consecutive entries of one V^T row.
           const float bv = bqkv[16 * ob + r16];
-          float4_t a0 = {bv, bv, bv, bv}, a1 = a0;
+          float4_t a[T];
 #pragma unroll
-          for (int ks = 0; ks < KS; ++ks) {
-            a0 = mfma16x16x32(xn[0][ks], cur[ks], a0);
-            a1 = mfma16x16x32(xn[1][ks], cur[ks], a1);
-          }
+          for (int t = 0; t < T; ++t) a[t] = float4_t{bv, bv, bv, bv};
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int t = 0; t < T; ++t) a[t] = mfma16x16x32(xn[t][ks], cur[ks], a[t]);
           const int fb = ob - 2 * FB;
-          *reinterpret_cast<half4_t*>(vt_lds + (16 * fb + r16) * LD + 16 * tb0 + 4 * g) = to_half4(a0);
-          *reinterpret_cast<half4_t*>(vt_lds + (16 * fb + r16) * LD + 16 * tb1 + 4 * g) = to_half4(a1);
+#pragma unroll
+          for (int t = 0; t < T; ++t)
+            *reinterpret_cast<half4_t*>(vt_lds + (16 * fb + r16) * LD + 16 * tblock(t) + 4 * g) = to_half4(a[t]);
         }
        }
       }
@@ -257,8 +279,8 @@ __global__ __launch_bounds__(256, 1) void fused_stack_kernel(
     // B operand of O^T = V^T . P^T directly.  S <= 128 keys, so all scores of a
     // query block fit in registers and the softmax needs no running rescale.
 #pragma unroll 1
-    for (int t = 0; t < 2; ++t) {
-      const int qb = t ? tb1 : tb0;
+    for (int t = 0; t < T; ++t) {
+      const int qb = tblock(t);
       const int query = 16 * qb + r16;
 #pragma unroll 1
       for (int h = 0; h < H; ++h) {
@@ -336,12 +358,12 @@ __global__ __launch_bounds__(256, 1) void fused_stack_kernel(
 
     // ---- output projection + residual (ctx from the wave's own LDS rows) -----
     {
-      half8_t cf[2][KS];
+      half8_t cf[T][KS];
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        cf[0][ks] = *reinterpret_cast<const half8_t*>(q_lds + (16 * tb0 + r16) * LD + 32 * ks + 8 * g);
-        cf[1][ks] = *reinterpret_cast<const half8_t*>(q_lds + (16 * tb1 + r16) * LD + 32 * ks + 8 * g);
-      }
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+          cf[t][ks] = *reinterpret_cast<const half8_t*>(q_lds + (16 * tblock(t) + r16) * LD + 32 * ks + 8 * g);
       gemm_accumulate<KS>(wo, bo, cf, res, wbuf_o, lane, g);
     }
 
@@ -349,7 +371,7 @@ __global__ __launch_bounds__(256, 1) void fused_stack_kernel(
     half8_t wbuf1[PF][KS];
     prefetch_head<KS>(w1, wbuf1, lane);
     layer_norm(res, g2, be2, xn, g);
-    half8_t hf[2][FKS];
+    half8_t hf[T][FKS];
     half8_t wbuf2[PF][FKS];
     {
 #pragma unroll
@@ -362,17 +384,17 @@ __global__ __launch_bounds__(256, 1) void fused_stack_kernel(
           for (int ks = 0; ks < KS; ++ks) wbuf1[ob % PF][ks] = frag(w1, (ob + PF) * KS + ks, lane);
         }
         const float4_t b = ld4(b1 + 16 * ob + 4 * g);
-        float4_t a0 = b, a1 = b;
+        float4_t a[T];
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          a0 = mfma16x16x32(cur[ks], xn[0][ks], a0);
-          a1 = mfma16x16x32(cur[ks], xn[1][ks], a1);
-        }
+        for (int t = 0; t < T; ++t) a[t] = b;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          hf[0][ob / 2][(ob & 1) * 4 + i] = (half_t)gelu_erf(a0[i]);
-          hf[1][ob / 2][(ob & 1) * 4 + i] = (half_t)gelu_erf(a1[i]);
-        }
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+          for (int t = 0; t < T; ++t) a[t] = mfma16x16x32(cur[ks], xn[t][ks], a[t]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int t = 0; t < T; ++t) hf[t][ob / 2][(ob & 1) * 4 + i] = (half_t)gelu_erf(a[t][i]);
         if (ob == 2 * FKS - PF - 1) prefetch_head<FKS>(w2, wbuf2, lane);
       }
     }
@@ -383,10 +405,10 @@ __global__ __launch_bounds__(256, 1) void fused_stack_kernel(
   const float* gf = ppack + layers * P_LAYER;
   const float* bf = gf + D;
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
+  for (int t = 0; t < T; ++t) {
     float mean, rstd;
     row_stats(res[t], mean, rstd);
-    const int tok = 16 * (t ? tb1 : tb0) + r16;
+    const int tok = 16 * tblock(t) + r16;
     if (tok < S) {
 #pragma unroll
       for (int fb = 0; fb < FB; ++fb) {
@@ -426,7 +448,8 @@ __global__ void pack_fragments_kernel(const float* __restrict__ w, half_t* __res
 template <int HD>
 static hipError_t launch(const float* x, float* y, const half_t* w, const float* p, int64_t batch, int S,
                          int layers, hipStream_t s) {
-  hipLaunchKernelGGL((fused_stack_kernel<HD>), dim3((unsigned)batch), dim3(256), 0, s, x, y, w, p, S, layers);
+  hipLaunchKernelGGL((fused_stack_kernel<HD, FUSED_WAVES>), dim3((unsigned)batch), dim3(64 * FUSED_WAVES), 0, s,
+                     x, y, w, p, S, layers);
   return hipGetLastError();
 }
 
