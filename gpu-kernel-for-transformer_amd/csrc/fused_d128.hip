@@ -12,20 +12,25 @@
 // Layout.  Eight waves (two per SIMD) each own one 16-token block: wave w
 // holds block w for w < 4 and block 11-w otherwise, so the two waves sharing
 // a SIMD (w and w+4) hold blocks b and 7-b and every SIMD gets the same causal
-// attention work.  (FUSED_WAVES=4 builds the one-wave-per-SIMD variant: wave w
-// owns blocks w and 7-w.)  The residual stream stays in
-// registers in the C layout of a "swapped" MFMA product out^T = W . act^T:
-// lane l holds token l%16 and features 16*fb + 4*(l/16) + i.  Read back as an
-// MFMA operand, that layout gives a k-step ks the reduction indices
-// 32ks + 4*(l/16) + (m & 3) + 16*(m >> 2) (m = 0..7); only the pairing of A's
-// and B's k index matters, so the weights multiplied by register-resident
-// activations are pre-packed in exactly that order ("permuted" packing, see
-// xb_pack_linear_fragments), fragment-major, one coalesced 16-byte load per
-// lane and MFMA operand.  Q, K and V^T are written to LDS by the QKV loop
-// (K and V^T are needed by every wave); the attention context overwrites the
-// wave's own Q rows and feeds the output projection from LDS in natural k
-// order (so Wo uses the "natural" packing).  LN outputs and the FFN hidden
-// activation never leave registers.
+// attention work.  The residual stream stays in registers in the C layout of
+// a "swapped" MFMA product out^T = W . act^T: lane l holds token l%16 and
+// features 16*fb + 4*(l/16) + i.  Read back as an MFMA operand, that layout
+// gives a k-step ks the reduction indices 32ks + 4*(l/16) + (m & 3) +
+// 16*(m >> 2) (m = 0..7); only the pairing of A's and B's k index matters, so
+// every weight is pre-packed in exactly that order ("permuted" packing, see
+// xb_pack_linear_fragments), fragment-major: one 16 x 32 fragment is 1 KB,
+// 16 bytes per lane.  Q and the attention context stay in registers in that
+// operand order; K is written to LDS with each k-step's 32 features in the
+// same order, V transposed.  LN outputs and the FFN hidden activation never
+// leave registers.
+//
+// Weights.  Every weight matrix (128 x 128 FP16, 32 KB) is copied once per
+// workgroup into one of two LDS stages by direct global -> LDS loads (4 per
+// wave), one matrix ahead of its use, and all eight waves read their
+// fragments from LDS.  The per-layer bias / LayerNorm vectors travel the same
+// way.  Inside the layer loop these copies are the only vector-memory
+// operations, so "vmcnt(0)" before a stage's barrier means exactly "this
+// stage has landed".
 #include "common.h"
 #include "../../include/xblock.h"
 
@@ -37,10 +42,6 @@ constexpr int KS = D / 32;      // k-steps over the model width
 constexpr int FB = D / 16;      // 16-wide feature blocks
 constexpr int SMAX = 128;
 constexpr int LD = D + 8;       // LDS row stride (halves) of Q/ctx, K and V^T (SMAX == D)
-
-__device__ __forceinline__ half8_t frag(const half_t* __restrict__ w, int idx, int lane) {
-  return *reinterpret_cast<const half8_t*>(w + ((size_t)idx * 64 + lane) * 8);
-}
 
 __device__ __forceinline__ float4_t ld4(const float* p) { return *reinterpret_cast<const float4_t*>(p); }
 
@@ -78,102 +79,77 @@ __device__ __forceinline__ void row_stats(const float4_t (&r)[FB], float& mean, 
   rstd = rsqrtf(q * (1.0f / D) + 1e-5f);
 }
 
-// LayerNorm of the wave's register-resident token blocks -> MFMA operands.
-template <int T>
-__device__ __forceinline__ void layer_norm(const float4_t (&res)[T][FB], const float* __restrict__ gamma,
-                                           const float* __restrict__ beta, half8_t (&xn)[T][KS], int g) {
+// LayerNorm of the wave's register-resident token block -> MFMA operands.
+// gamma / beta are LDS-resident.
+__device__ __forceinline__ void layer_norm(const float4_t (&res)[FB], const float* gamma, const float* beta,
+                                           half8_t (&xn)[KS], int g) {
+  float mean, rstd;
+  row_stats(res, mean, rstd);
 #pragma unroll
-  for (int t = 0; t < T; ++t) {
-    float mean, rstd;
-    row_stats(res[t], mean, rstd);
+  for (int ks = 0; ks < KS; ++ks) {
+    float4_t lo, hi;
+    const float4_t g0 = ld4(gamma + 32 * ks + 4 * g), g1 = ld4(gamma + 32 * ks + 16 + 4 * g);
+    const float4_t b0 = ld4(beta + 32 * ks + 4 * g), b1 = ld4(beta + 32 * ks + 16 + 4 * g);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      float4_t lo, hi;
-      const float4_t g0 = ld4(gamma + 32 * ks + 4 * g), g1 = ld4(gamma + 32 * ks + 16 + 4 * g);
-      const float4_t b0 = ld4(beta + 32 * ks + 4 * g), b1 = ld4(beta + 32 * ks + 16 + 4 * g);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        lo[i] = (res[t][2 * ks][i] - mean) * rstd * g0[i] + b0[i];
-        hi[i] = (res[t][2 * ks + 1][i] - mean) * rstd * g1[i] + b1[i];
-      }
-      xn[t][ks] = to_operand(lo, hi);
+    for (int i = 0; i < 4; ++i) {
+      lo[i] = (res[2 * ks][i] - mean) * rstd * g0[i] + b0[i];
+      hi[i] = (res[2 * ks + 1][i] - mean) * rstd * g1[i] + b1[i];
     }
+    xn[ks] = to_operand(lo, hi);
   }
 }
 
-// Waves per workgroup: 8 (two per SIMD, one 16-token block each) or 4 (one
-// per SIMD, two token blocks each).
-#ifndef FUSED_WAVES
-#define FUSED_WAVES 8
-#endif
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void global_void_t;
 
-// Weight fragments stream from L2 with PF output blocks in flight: the loads
-// for block ob + PF are issued before block ob's MFMAs.  With one wave per
-// SIMD nothing else hides their latency, so that layout prefetches deeper.
-#ifndef FUSED_PF
-#define FUSED_PF (FUSED_WAVES == 8 ? 2 : 4)
-#endif
-constexpr int PF = FUSED_PF;
-
-// Fragments of output blocks [0, PF) of a weight with KIN k-steps.
-template <int KIN>
-__device__ __forceinline__ void prefetch_head(const half_t* __restrict__ w, half8_t (&buf)[PF][KIN], int lane) {
-#pragma unroll
-  for (int j = 0; j < PF; ++j)
-#pragma unroll
-    for (int ks = 0; ks < KIN; ++ks) buf[j][ks] = frag(w, j * KIN + ks, lane);
+// One 16-byte-per-lane direct global -> LDS load: lane i's bytes land at
+// lds_wave_base + 16 i.  The LDS base must be wave-uniform.
+__device__ __forceinline__ void dma16(const void* src_lane, void* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds((global_void_t*)src_lane, (lds_void_t*)lds_wave_base, 16, 0, 0);
 }
 
-// res[t][ob] += (W . act^T)[ob] + bias over all FB output blocks; `buf` holds
-// the fragments of blocks 0..PF-1 on entry (prefetch_head).
-template <int KIN, int T>
-__device__ __forceinline__ void gemm_accumulate(const half_t* __restrict__ w, const float* __restrict__ bias,
-                                                const half8_t (&act)[T][KIN], float4_t (&res)[T][FB],
-                                                half8_t (&buf)[PF][KIN], int lane, int g) {
-#pragma unroll
-  for (int ob = 0; ob < FB; ++ob) {
-    half8_t cur[KIN];
-#pragma unroll
-    for (int ks = 0; ks < KIN; ++ks) cur[ks] = buf[ob % PF][ks];
-    if (ob + PF < FB) {
-#pragma unroll
-      for (int ks = 0; ks < KIN; ++ks) buf[ob % PF][ks] = frag(w, (ob + PF) * KIN + ks, lane);
-    }
-    float4_t a[T];
-#pragma unroll
-    for (int t = 0; t < T; ++t) a[t] = float4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < KIN; ++ks)
-#pragma unroll
-      for (int t = 0; t < T; ++t) a[t] = mfma16x16x32(cur[ks], act[t][ks], a[t]);
-    const float4_t b = ld4(bias + 16 * ob + 4 * g);
-#pragma unroll
-    for (int t = 0; t < T; ++t) res[t][ob] += a[t] + b;
-  }
+// Workgroup barrier after this wave's DMA loads and LDS accesses completed.
+// (__syncthreads would also do; spelled out because the waits matter.)
+__device__ __forceinline__ void drain_and_barrier() {
+  __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (0 << 8) | (0 << 14));  // vmcnt(0) expcnt(7) lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
-template <int HD, int NW>
+constexpr int NW = 8;                  // waves per workgroup (two per SIMD)
+constexpr int F = 128;                 // ffn_dim (the packed-layer strides assume it)
+constexpr int FKS = F / 32;
+constexpr int MATS = 6;                // Wq Wk Wv Wo W1 W2 per layer, each 128 x 128
+constexpr int MAT_FRAGS = D / 16 * KS; // 32 fragments of 16 x 32 halves (1 KB each)
+constexpr int MAT_BYTES = MAT_FRAGS * 1024;
+constexpr int P_LAYER = 9 * D + F;     // bq bk bv bo b1 b2 g1 be1 g2 be2 (floats)
+constexpr int P_BQ = 0, P_BK = D, P_BV = 2 * D, P_BO = 3 * D, P_B1 = 4 * D, P_B2 = 4 * D + F;
+constexpr int P_G1 = 5 * D + F, P_BE1 = 6 * D + F, P_G2 = 7 * D + F, P_BE2 = 8 * D + F;
+static_assert(P_LAYER * 4 == NW * 40 * 16, "layer vectors: 40 lanes x 16 bytes per wave");
+static_assert(2 * D * 4 == NW * 8 * 16, "final LayerNorm vectors: 8 lanes x 16 bytes per wave");
+
+// Fragment `idx` of a staged matrix: 1 KB, lane-contiguous.
+__device__ __forceinline__ half8_t sfrag(const char* stage, int idx, int lane) {
+  return *reinterpret_cast<const half8_t*>(stage + idx * 1024 + lane * 16);
+}
+
+template <int HD>
 __global__ __launch_bounds__(64 * NW, 1) void fused_stack_kernel(
     const float* __restrict__ x, float* __restrict__ y, const half_t* __restrict__ wpack,
     const float* __restrict__ ppack, int S, int layers) {
-  constexpr int F = 128;  // ffn_dim (the packed-layer strides below assume it)
-  constexpr int T = 8 / NW;  // 16-token blocks per wave
   constexpr int H = D / HD;
-  constexpr int FKS = F / 32;
-  constexpr int HDB = HD < 16 ? 1 : HD / 16;   // 16-row blocks of one head in V^T / ctx
+  constexpr int HDB = HD < 16 ? 1 : HD / 16;   // 16-row blocks of one head in V^T
   constexpr int KSH = HD >= 32 ? HD / 32 : 1;  // k-steps of one head's q.k
-  constexpr int64_t W_LAYER = 4 * D * D + 2 * (int64_t)F * D;
-  constexpr int P_LAYER = 9 * D + F;
-  __shared__ __attribute__((aligned(16))) half_t q_lds[SMAX * LD];   // Q (pre-scaled), then ctx
-  __shared__ __attribute__((aligned(16))) half_t k_lds[SMAX * LD];   // K, row-major
+  __shared__ __attribute__((aligned(16))) half_t k_lds[SMAX * LD];   // K [token][feature, permuted per k-step]
   __shared__ __attribute__((aligned(16))) half_t vt_lds[D * LD];     // V^T [feature][token]
+  __shared__ __attribute__((aligned(1024))) char wst[2][MAT_BYTES];  // weight matrix stages
+  __shared__ __attribute__((aligned(16))) float prm[2][P_LAYER];     // per-layer vectors, by layer parity
 
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int g = lane / 16, r16 = lane % 16;
-  // Token block of the wave's t-th block.  Four waves: w and 7-w.  Eight waves
-  // (two per SIMD, waves w and w+4 sharing one): w for w < 4, else 11-w, so
-  // every SIMD again holds blocks b and 7-b.
-  auto tblock = [&](int t) { return NW == 4 ? (t ? 7 - wave : wave) : (wave < 4 ? wave : 11 - wave); };
+  const int tb = wave < 4 ? wave : 11 - wave;  // SIMD w holds blocks w and 7-w
   // Additive causal mask of a diagonal 16x16 block: key 4g + i vs query r16.
   float4_t diag_mask;
 #pragma unroll
@@ -181,243 +157,238 @@ __global__ __launch_bounds__(64 * NW, 1) void fused_stack_kernel(
   const int64_t seq = blockIdx.x;
   const float* xs = x + seq * S * D;
   float* ys = y + seq * S * D;
+  const int groups = layers * MATS;
 
-  // Residual stream, C layout: res[t][fb][i] = x[16 tb_t + r16][16 fb + 4 g + i].
-  float4_t res[T][FB];
+  // Weight group gi = matrix gi % 6 of layer gi / 6 into stage gi & 1; each
+  // wave moves fragments wave, wave+8, ... .  The W2 group also carries the
+  // next layer's vectors (or the final LayerNorm's) into prm[(layer+1) & 1].
+  auto issue_group = [&](int gi) {
+    const int layer = gi / MATS, m = gi % MATS;
+    const half_t* src = wpack + ((int64_t)layer * MATS + m) * MAT_FRAGS * 512;
 #pragma unroll
-  for (int t = 0; t < T; ++t) {
-    const int tok = 16 * tblock(t) + r16;
-#pragma unroll
-    for (int fb = 0; fb < FB; ++fb)
-      res[t][fb] = tok < S ? ld4(xs + (int64_t)tok * D + 16 * fb + 4 * g) : float4_t{0.f, 0.f, 0.f, 0.f};
-  }
-
-  for (int layer = 0; layer < layers; ++layer) {
-    const half_t* wqkv = wpack + layer * W_LAYER;  // Wq, Wk, Wv: 24 blocks of 16 output features
-    const half_t* wo = wqkv + 3 * D * D;
-    const half_t* w1 = wo + D * D;
-    const half_t* w2 = w1 + F * D;
-    const float* pp = ppack + layer * P_LAYER;
-    const float* bqkv = pp;  // bq, bk, bv back to back
-    const float* bo = pp + 3 * D;
-    const float* b1 = pp + 4 * D;
-    const float* b2 = pp + 4 * D + F;
-    const float* g1 = pp + 5 * D + F;
-    const float* be1 = pp + 6 * D + F;
-    const float* g2 = pp + 7 * D + F;
-    const float* be2 = pp + 8 * D + F;
-
-    // ---- LN1 and the QKV projection into LDS ------------------------------
-    half8_t xn[T][KS];
-    layer_norm(res, g1, be1, xn, g);
-    __syncthreads();  // the previous layer's attention has finished reading K / V^T
-    {
-      // 24 output blocks (Q, K, V) in groups of PF: group G+1's fragments load
-      // while group G's MFMAs run.
-      half8_t wbuf[PF][KS];
-      prefetch_head<KS>(wqkv, wbuf, lane);
-#pragma unroll 1
-      for (int ob0 = 0; ob0 < 3 * FB; ob0 += PF) {
-       half8_t wcur[PF][KS];
-#pragma unroll
-       for (int j = 0; j < PF; ++j)
-#pragma unroll
-         for (int ks = 0; ks < KS; ++ks) wcur[j][ks] = wbuf[j][ks];
-       if (ob0 + PF < 3 * FB) {
-#pragma unroll
-         for (int j = 0; j < PF; ++j)
-#pragma unroll
-           for (int ks = 0; ks < KS; ++ks) wbuf[j][ks] = frag(wqkv, (ob0 + PF + j) * KS + ks, lane);
-       }
-#pragma unroll
-       for (int j = 0; j < PF; ++j) {
-        const int ob = ob0 + j;
-        const half8_t (&cur)[KS] = wcur[j];
-        if (ob < 2 * FB) {
-          // Q / K: swapped product, lane = (token r16, features 16fb + 4g + i).
-          // Q's weights and bias arrive pre-multiplied by scale * log2(e).
-          const float4_t b = ld4(bqkv + 16 * ob + 4 * g);
-          float4_t a[T];
-#pragma unroll
-          for (int t = 0; t < T; ++t) a[t] = b;
-#pragma unroll
-          for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-            for (int t = 0; t < T; ++t) a[t] = mfma16x16x32(cur[ks], xn[t][ks], a[t]);
-          const int fb = ob % FB;
-          half_t* dst = ob < FB ? q_lds : k_lds;
-#pragma unroll
-          for (int t = 0; t < T; ++t)
-            *reinterpret_cast<half4_t*>(dst + (16 * tblock(t) + r16) * LD + 16 * fb + 4 * g) = to_half4(a[t]);
-        } else {
-          // V: unswapped product, lane = (tokens 16tb + 4g + i, feature 16fb + r16),
-          // i.e. four consecutive entries of one V^T row.
-          const float bv = bqkv[16 * ob + r16];
-          float4_t a[T];
-#pragma unroll
-          for (int t = 0; t < T; ++t) a[t] = float4_t{bv, bv, bv, bv};
-#pragma unroll
-          for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-            for (int t = 0; t < T; ++t) a[t] = mfma16x16x32(xn[t][ks], cur[ks], a[t]);
-          const int fb = ob - 2 * FB;
-#pragma unroll
-          for (int t = 0; t < T; ++t)
-            *reinterpret_cast<half4_t*>(vt_lds + (16 * fb + r16) * LD + 16 * tblock(t) + 4 * g) = to_half4(a[t]);
-        }
-       }
+    for (int j = 0; j < MAT_FRAGS / NW; ++j) {
+      const int f = wave + NW * j;
+      dma16(src + (f * 64 + lane) * 8, wst[gi & 1] + f * 1024);
+    }
+    if (m == MATS - 1) {
+      float* dst = prm[(layer + 1) & 1];
+      if (layer + 1 < layers) {
+        if (lane < 40) dma16(ppack + (int64_t)(layer + 1) * P_LAYER + wave * 160 + lane * 4, dst + wave * 160);
+      } else {
+        if (lane < 8) dma16(ppack + (int64_t)layers * P_LAYER + wave * 32 + lane * 4, dst + wave * 32);
       }
     }
-    // The output projection's first fragments load during attention.
-    half8_t wbuf_o[PF][KS];
-    prefetch_head<KS>(wo, wbuf_o, lane);
-    __syncthreads();
+  };
+  // Start of group gi: its loads (issued one group earlier) have landed and
+  // every wave is done with group gi-1's stage, which now receives gi+1.
+  auto begin_group = [&](int gi) -> const char* {
+    drain_and_barrier();
+    if (gi + 1 < groups) issue_group(gi + 1);
+    return wst[gi & 1];
+  };
 
-    // ---- causal attention of the wave's query blocks, every head ------------
+  // Residual stream, C layout: res[fb][i] = x[16 tb + r16][16 fb + 4 g + i].
+  float4_t res[FB];
+  {
+    const int tok = 16 * tb + r16;
+#pragma unroll
+    for (int fb = 0; fb < FB; ++fb)
+      res[fb] = tok < S ? ld4(xs + (int64_t)tok * D + 16 * fb + 4 * g) : float4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  if (lane < 40) dma16(ppack + wave * 160 + lane * 4, prm[0] + wave * 160);
+  issue_group(0);
+  drain_and_barrier();
+
+  for (int layer = 0; layer < layers; ++layer) {
+    const float* pp = prm[layer & 1];
+    const int g0 = layer * MATS;
+    half8_t xn[KS];
+    layer_norm(res, pp + P_G1, pp + P_BE1, xn, g);
+
+    // ---- Q: kept in registers as MFMA operands (permuted k order) ----------
+    half8_t qop[KS];
+    {
+      const char* st = begin_group(g0 + 0);
+      float4_t qc[FB];
+#pragma unroll
+      for (int ob = 0; ob < FB; ++ob) {
+        float4_t a = ld4(pp + P_BQ + 16 * ob + 4 * g);  // Wq, bq carry scale * log2(e)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) a = mfma16x16x32(sfrag(st, ob * KS + ks, lane), xn[ks], a);
+        qc[ob] = a;
+      }
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) qop[ks] = to_operand(qc[2 * ks], qc[2 * ks + 1]);
+    }
+    // ---- K: LDS row-major, each k-step's 32 features in the permuted order --
+    {
+      const char* st = begin_group(g0 + 1);
+#pragma unroll
+      for (int ob = 0; ob < FB; ++ob) {
+        float4_t a = ld4(pp + P_BK + 16 * ob + 4 * g);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) a = mfma16x16x32(sfrag(st, ob * KS + ks, lane), xn[ks], a);
+        // features 32 (ob/2) + 16 (ob&1) + 4g + i sit at 32 (ob/2) + 8g + 4 (ob&1) + i
+        *reinterpret_cast<half4_t*>(k_lds + (16 * tb + r16) * LD + 32 * (ob / 2) + 8 * g + 4 * (ob & 1)) = to_half4(a);
+      }
+    }
+    // ---- V: unswapped product, lane = four consecutive entries of a V^T row --
+    {
+      const char* st = begin_group(g0 + 2);
+#pragma unroll
+      for (int ob = 0; ob < FB; ++ob) {
+        const float bv = pp[P_BV + 16 * ob + r16];
+        float4_t a = {bv, bv, bv, bv};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) a = mfma16x16x32(xn[ks], sfrag(st, ob * KS + ks, lane), a);
+        *reinterpret_cast<half4_t*>(vt_lds + (16 * ob + r16) * LD + 16 * tb + 4 * g) = to_half4(a);
+      }
+    }
+    __syncthreads();  // K and V^T of every token block are in LDS
+
+    // ---- causal attention of the wave's query block, every head -------------
     // S^T = K . Q^T (M = keys, N = queries): lane holds keys 16kb + 4g + i of
     // query r16, which with the key order 32kt + 4g + (m&3) + 16(m>>2) is the
     // B operand of O^T = V^T . P^T directly.  S <= 128 keys, so all scores of a
     // query block fit in registers and the softmax needs no running rescale.
-#pragma unroll 1
-    for (int t = 0; t < T; ++t) {
-      const int qb = tblock(t);
-      const int query = 16 * qb + r16;
-#pragma unroll 1
-      for (int h = 0; h < H; ++h) {
-        const int ks0 = (h * HD) / 32;
-        half8_t qh[KSH];
+    // The context leaves as MFMA operands in the permuted k order (cop).
+    const int qb = tb;
+    half8_t cop[KS];
 #pragma unroll
-        for (int j = 0; j < KSH; ++j) {
-          qh[j] = *reinterpret_cast<const half8_t*>(q_lds + query * LD + 32 * (ks0 + j) + 8 * g);
-          if constexpr (HD < 32) {  // keep only this head's features of the shared k-step
+    for (int ks = 0; ks < KS; ++ks) cop[ks] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-            for (int m = 0; m < 8; ++m)
-              if ((32 * ks0 + 8 * g + m) / HD != h) qh[j][m] = (half_t)0.f;
+    for (int h = 0; h < H; ++h) {
+      const int ks0 = (h * HD) / 32;
+      half8_t qh[KSH];
+#pragma unroll
+      for (int j = 0; j < KSH; ++j) {
+        qh[j] = qop[ks0 + j];
+        if constexpr (HD < 32) {  // keep only this head's features of the shared k-step
+#pragma unroll
+          for (int m = 0; m < 8; ++m)
+            if ((32 * ks0 + 4 * g + (m & 3) + 16 * (m >> 2)) / HD != h) qh[j][m] = (half_t)0.f;
+        }
+      }
+      float4_t s[8];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 8; ++kb) {
+        s[kb] = float4_t{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        if (kb <= qb) {
+          float4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int j = 0; j < KSH; ++j) {
+            const half8_t kf = *reinterpret_cast<const half8_t*>(k_lds + (16 * kb + r16) * LD + 32 * (ks0 + j) + 8 * g);
+            acc = mfma16x16x32(kf, qh[j], acc);
+          }
+          if (kb == qb) acc += diag_mask;  // -inf above the diagonal
+          s[kb] = acc;
+          mx = fmaxf(mx, fmaxf(fmaxf(acc[0], acc[1]), fmaxf(acc[2], acc[3])));
+        }
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      float lsum = 0.f;
+      const int vrow0 = HD < 16 ? 16 * (h / 2) : h * HD;
+      float4_t o[HDB];
+#pragma unroll
+      for (int hb = 0; hb < HDB; ++hb) o[hb] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        if (2 * kt <= qb) {
+          float4_t p0, p1;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            p0[i] = __builtin_amdgcn_exp2f(s[2 * kt][i] - mx);
+            p1[i] = __builtin_amdgcn_exp2f(s[2 * kt + 1][i] - mx);  // exp2(-inf) = 0 past qb
+          }
+          lsum += ((p0[0] + p0[1]) + (p0[2] + p0[3])) + ((p1[0] + p1[1]) + (p1[2] + p1[3]));
+          const half8_t pf = to_operand(p0, p1);
+#pragma unroll
+          for (int hb = 0; hb < HDB; ++hb) {
+            const half_t* vr = vt_lds + (vrow0 + 16 * hb + r16) * LD + 32 * kt + 4 * g;
+            const half8_t vf = cat4(*reinterpret_cast<const half4_t*>(vr), *reinterpret_cast<const half4_t*>(vr + 16));
+            o[hb] = mfma16x16x32(vf, pf, o[hb]);
           }
         }
-        float4_t s[8];
-        float mx = -INFINITY;
+      }
+      lsum += __shfl_xor(lsum, 16);
+      lsum += __shfl_xor(lsum, 32);
+      const float inv = 1.0f / lsum;
+      // O^T C layout: lane holds features vrow0 + 16hb + 4g + i of query r16;
+      // block 16c belongs to k-step c/2, half c&1 of the permuted operand.
+      if constexpr (HD >= 16) {
 #pragma unroll
-        for (int kb = 0; kb < 8; ++kb) {
-          s[kb] = float4_t{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-          if (kb <= qb) {
-            float4_t acc = {0.f, 0.f, 0.f, 0.f};
+        for (int hb = 0; hb < HDB; ++hb) {
+          const int c = (vrow0 + 16 * hb) / 16;
+          const half4_t v = to_half4(o[hb] * inv);
 #pragma unroll
-            for (int j = 0; j < KSH; ++j) {
-              const half8_t kf =
-                  *reinterpret_cast<const half8_t*>(k_lds + (16 * kb + r16) * LD + 32 * (ks0 + j) + 8 * g);
-              acc = mfma16x16x32(kf, qh[j], acc);
-            }
-            if (kb == qb) acc += diag_mask;  // -inf above the diagonal
-            s[kb] = acc;
-            mx = fmaxf(mx, fmaxf(fmaxf(acc[0], acc[1]), fmaxf(acc[2], acc[3])));
-          }
+          for (int i = 0; i < 4; ++i) cop[c / 2][4 * (c & 1) + i] = v[i];
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        float lsum = 0.f;
-        const int vrow0 = HD < 16 ? 16 * (h / 2) : h * HD;
-        float4_t o[HDB];
+      } else {
+        // Two 8-wide heads share one 16-row block: rows 0-7 (g < 2) are the even head's.
+        const int c = vrow0 / 16;
+        if ((g / 2) == (h & 1)) {
+          const half4_t v = to_half4(o[0] * inv);
 #pragma unroll
-        for (int hb = 0; hb < HDB; ++hb) o[hb] = float4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
-          if (2 * kt <= qb) {
-            float4_t p0, p1;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              p0[i] = __builtin_amdgcn_exp2f(s[2 * kt][i] - mx);
-              p1[i] = __builtin_amdgcn_exp2f(s[2 * kt + 1][i] - mx);  // exp2(-inf) = 0 past qb
-            }
-            lsum += ((p0[0] + p0[1]) + (p0[2] + p0[3])) + ((p1[0] + p1[1]) + (p1[2] + p1[3]));
-            const half8_t pf = to_operand(p0, p1);
-#pragma unroll
-            for (int hb = 0; hb < HDB; ++hb) {
-              const half_t* vr = vt_lds + (vrow0 + 16 * hb + r16) * LD + 32 * kt + 4 * g;
-              const half8_t vf = cat4(*reinterpret_cast<const half4_t*>(vr), *reinterpret_cast<const half4_t*>(vr + 16));
-              o[hb] = mfma16x16x32(vf, pf, o[hb]);
-            }
-          }
-        }
-        lsum += __shfl_xor(lsum, 16);
-        lsum += __shfl_xor(lsum, 32);
-        const float inv = 1.0f / lsum;
-        // O^T C layout: rows 4g + i of block (vrow0 + 16hb) for query r16. The
-        // wave's own Q rows of this head are consumed, so ctx overwrites them.
-        if constexpr (HD >= 16) {
-#pragma unroll
-          for (int hb = 0; hb < HDB; ++hb)
-            *reinterpret_cast<half4_t*>(q_lds + query * LD + vrow0 + 16 * hb + 4 * g) = to_half4(o[hb] * inv);
-        } else {
-          // Two 8-wide heads share one 16-row block: rows 0-7 (g < 2) are the even head's.
-          if ((g / 2) == (h & 1))
-            *reinterpret_cast<half4_t*>(q_lds + query * LD + vrow0 + 4 * g) = to_half4(o[0] * inv);
+          for (int i = 0; i < 4; ++i) cop[c / 2][4 * (c & 1) + i] = v[i];
         }
       }
     }
 
-    // ---- output projection + residual (ctx from the wave's own LDS rows) -----
+    // ---- output projection + residual (Wo in permuted packing) ---------------
     {
-      half8_t cf[T][KS];
+      const char* st = begin_group(g0 + 3);
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
+      for (int ob = 0; ob < FB; ++ob) {
+        float4_t a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int t = 0; t < T; ++t)
-          cf[t][ks] = *reinterpret_cast<const half8_t*>(q_lds + (16 * tblock(t) + r16) * LD + 32 * ks + 8 * g);
-      gemm_accumulate<KS>(wo, bo, cf, res, wbuf_o, lane, g);
+        for (int ks = 0; ks < KS; ++ks) a = mfma16x16x32(sfrag(st, ob * KS + ks, lane), cop[ks], a);
+        res[ob] += a + ld4(pp + P_BO + 16 * ob + 4 * g);
+      }
     }
 
     // ---- LN2, FFN: gelu(n2 W1^T + b1) W2^T + b2 + residual ----------------
-    half8_t wbuf1[PF][KS];
-    prefetch_head<KS>(w1, wbuf1, lane);
-    layer_norm(res, g2, be2, xn, g);
-    half8_t hf[T][FKS];
-    half8_t wbuf2[PF][FKS];
+    layer_norm(res, pp + P_G2, pp + P_BE2, xn, g);
+    half8_t hf[FKS];
     {
+      const char* st = begin_group(g0 + 4);
 #pragma unroll
       for (int ob = 0; ob < 2 * FKS; ++ob) {
-        half8_t cur[KS];
+        float4_t a = ld4(pp + P_B1 + 16 * ob + 4 * g);
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) cur[ks] = wbuf1[ob % PF][ks];
-        if (ob + PF < 2 * FKS) {
+        for (int ks = 0; ks < KS; ++ks) a = mfma16x16x32(sfrag(st, ob * KS + ks, lane), xn[ks], a);
 #pragma unroll
-          for (int ks = 0; ks < KS; ++ks) wbuf1[ob % PF][ks] = frag(w1, (ob + PF) * KS + ks, lane);
-        }
-        const float4_t b = ld4(b1 + 16 * ob + 4 * g);
-        float4_t a[T];
-#pragma unroll
-        for (int t = 0; t < T; ++t) a[t] = b;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-          for (int t = 0; t < T; ++t) a[t] = mfma16x16x32(cur[ks], xn[t][ks], a[t]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int t = 0; t < T; ++t) hf[t][ob / 2][(ob & 1) * 4 + i] = (half_t)gelu_erf(a[t][i]);
-        if (ob == 2 * FKS - PF - 1) prefetch_head<FKS>(w2, wbuf2, lane);
+        for (int i = 0; i < 4; ++i) hf[ob / 2][(ob & 1) * 4 + i] = (half_t)gelu_erf(a[i]);
       }
     }
-    gemm_accumulate<FKS>(w2, b2, hf, res, wbuf2, lane, g);
+    {
+      const char* st = begin_group(g0 + 5);
+#pragma unroll
+      for (int ob = 0; ob < FB; ++ob) {
+        float4_t a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < FKS; ++ks) a = mfma16x16x32(sfrag(st, ob * FKS + ks, lane), hf[ks], a);
+        res[ob] += a + ld4(pp + P_B2 + 16 * ob + 4 * g);
+      }
+    }
   }
 
-  // ---- final LayerNorm, FP32 output -----------------------------------------
-  const float* gf = ppack + layers * P_LAYER;
+  // ---- final LayerNorm, FP32 output (vectors arrived with the last group) ----
+  drain_and_barrier();
+  const float* gf = prm[layers & 1];
   const float* bf = gf + D;
+  float mean, rstd;
+  row_stats(res, mean, rstd);
+  const int tok = 16 * tb + r16;
+  if (tok < S) {
 #pragma unroll
-  for (int t = 0; t < T; ++t) {
-    float mean, rstd;
-    row_stats(res[t], mean, rstd);
-    const int tok = 16 * tblock(t) + r16;
-    if (tok < S) {
+    for (int fb = 0; fb < FB; ++fb) {
+      const float4_t gg = ld4(gf + 16 * fb + 4 * g), bb = ld4(bf + 16 * fb + 4 * g);
+      float4_t o;
 #pragma unroll
-      for (int fb = 0; fb < FB; ++fb) {
-        const float4_t gg = ld4(gf + 16 * fb + 4 * g), bb = ld4(bf + 16 * fb + 4 * g);
-        float4_t o;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) o[i] = (res[t][fb][i] - mean) * rstd * gg[i] + bb[i];
-        *reinterpret_cast<float4_t*>(ys + (int64_t)tok * D + 16 * fb + 4 * g) = o;
-      }
+      for (int i = 0; i < 4; ++i) o[i] = (res[fb][i] - mean) * rstd * gg[i] + bb[i];
+      *reinterpret_cast<float4_t*>(ys + (int64_t)tok * D + 16 * fb + 4 * g) = o;
     }
   }
 }
@@ -448,8 +419,7 @@ __global__ void pack_fragments_kernel(const float* __restrict__ w, half_t* __res
 template <int HD>
 static hipError_t launch(const float* x, float* y, const half_t* w, const float* p, int64_t batch, int S,
                          int layers, hipStream_t s) {
-  hipLaunchKernelGGL((fused_stack_kernel<HD, FUSED_WAVES>), dim3((unsigned)batch), dim3(64 * FUSED_WAVES), 0, s,
-                     x, y, w, p, S, layers);
+  hipLaunchKernelGGL((fused_stack_kernel<HD>), dim3((unsigned)batch), dim3(64 * NW), 0, s, x, y, w, p, S, layers);
   return hipGetLastError();
 }
 

@@ -201,7 +201,7 @@ class UserOptimizedTransformer(nn.Module):
                 q_scale = att.scale * _LOG2E
                 for lin in (att.q_proj, att.k_proj, att.v_proj, att.out_proj, layer.ffn_in, layer.ffn_out):
                     weights.append(kernels.pack_linear_fragments(
-                        lin.weight, natural=lin is att.out_proj, scale=q_scale if lin is att.q_proj else 1.0))
+                        lin.weight, scale=q_scale if lin is att.q_proj else 1.0))
                 vectors.append(att.q_proj.bias.detach().float() * q_scale)
                 for vec in (att.k_proj.bias, att.v_proj.bias, att.out_proj.bias,
                             layer.ffn_in.bias, layer.ffn_out.bias, layer.norm1.weight, layer.norm1.bias,

@@ -115,9 +115,9 @@ int xb_pack_linear_fragments(const float* w, void* out, int32_t n, int32_t k,
  * written once.  Same math as the per-op sequence above (FP16 MFMA operands,
  * FP32 accumulation / residual / softmax, exact-erf GELU).
  *   wpack: per layer, fragment-packed (xb_pack_linear_fragments) Wq, Wk, Wv,
- *          Wo [128,128], W1 [ffn,128], W2 [128,ffn], layers back to back; Wo
- *          in XB_PACK_NATURAL order, the others in XB_PACK_PERMUTED order;
- *          Wq packed with scale = softmax_scale * log2(e);
+ *          Wo [128,128], W1 [ffn,128], W2 [128,ffn], layers back to back, all
+ *          in XB_PACK_PERMUTED order; Wq packed with
+ *          scale = softmax_scale * log2(e);
  *   ppack: FP32, per layer bq * softmax_scale * log2(e), bk, bv, bo [128],
  *          b1 [ffn], b2 [128], norm1 gamma, beta, norm2 gamma, beta [128
  *          each]; then final_norm gamma, beta.
