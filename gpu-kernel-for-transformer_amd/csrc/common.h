@@ -47,19 +47,45 @@ __device__ __forceinline__ float group_max(float v) {
 // from Abramowitz & Stegun, Handbook of Mathematical Functions, eq. 7.1.26:
 //   erfc(z) ~= (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) exp(-z^2),
 //   t = 1 / (1 + p z), z >= 0, |error| <= 1.5e-7,
-// evaluated with one reciprocal and one exp2 (about 14 VALU instructions
+// evaluated with one reciprocal and one exp2 (about 13 VALU instructions
 // instead of a full-range erff).  The result feeds an FP16 store, whose
 // rounding (2^-11 relative) is far above this approximation error.
 __device__ __forceinline__ float gelu_erf(float x) {
   constexpr float kP = 0.3275911f * 0.70710678118654752440f;  // p / sqrt 2, z = |x| / sqrt 2
-  constexpr float a1 = 0.254829592f, a2 = -0.284496736f, a3 = 1.421413741f;
-  constexpr float a4 = -1.453152027f, a5 = 1.061405429f;
-  const float t = __builtin_amdgcn_rcpf(fmaf(fabsf(x), kP, 1.0f));
-  const float poly = t * fmaf(fmaf(fmaf(fmaf(a5, t, a4), t, a3), t, a2), t, a1);
+  // A&S coefficients halved: h = 0.5 erfc(|x| / sqrt 2) = t (b1 + t (b2 + ...)) exp(-x^2 / 2)
+  constexpr float b1 = 0.5f * 0.254829592f, b2 = 0.5f * -0.284496736f, b3 = 0.5f * 1.421413741f;
+  constexpr float b4 = 0.5f * -1.453152027f, b5 = 0.5f * 1.061405429f;
+  const float ax = fabsf(x);
+  const float t = __builtin_amdgcn_rcpf(fmaf(ax, kP, 1.0f));
+  const float poly = t * fmaf(fmaf(fmaf(fmaf(b5, t, b4), t, b3), t, b2), t, b1);
   // exp(-z^2) = exp(-x^2 / 2) = 2^(-x^2 * log2(e) / 2)
-  const float half_erfc = 0.5f * poly * __builtin_amdgcn_exp2f(x * x * -0.72134752044448170368f);
-  const float phi = x >= 0.f ? 1.0f - half_erfc : half_erfc;
-  return x * phi;
+  const float h = poly * __builtin_amdgcn_exp2f(x * x * -0.72134752044448170368f);
+  // x Phi(x) is x (1 - h) for x >= 0 and x h below: max(x, 0) - |x| h
+  return fmaf(-ax, h, fmaxf(x, 0.f));
 }
+
+// Cross-lane reductions over lanes l, l^16, l^32, l^48 with the gfx950 lane
+// swaps (VALU, no LDS round trip).  With both operands equal to v,
+// v_permlane16_swap leaves {v, v[l^16]} and v_permlane32_swap {v, v[l^32]}
+// in its two results, in some order per lane.
+__device__ __forceinline__ float xor16_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor16_max(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// Sum / max over the four 16-lane groups (lanes with the same l % 16).
+__device__ __forceinline__ float quad_group_sum(float v) { return xor32_sum(xor16_sum(v)); }
+__device__ __forceinline__ float quad_group_max(float v) { return xor32_max(xor16_max(v)); }
 
 }  // namespace xb

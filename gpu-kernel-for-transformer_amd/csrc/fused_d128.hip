@@ -66,17 +66,13 @@ __device__ __forceinline__ void row_stats(const float4_t (&r)[FB], float& mean, 
   float s = 0.f;
 #pragma unroll
   for (int fb = 0; fb < FB; ++fb) s += (r[fb][0] + r[fb][1]) + (r[fb][2] + r[fb][3]);
-  s += __shfl_xor(s, 16);
-  s += __shfl_xor(s, 32);
-  mean = s * (1.0f / D);
+  mean = quad_group_sum(s) * (1.0f / D);
   float q = 0.f;
 #pragma unroll
   for (int fb = 0; fb < FB; ++fb)
 #pragma unroll
     for (int i = 0; i < 4; ++i) { const float c = r[fb][i] - mean; q += c * c; }
-  q += __shfl_xor(q, 16);
-  q += __shfl_xor(q, 32);
-  rstd = rsqrtf(q * (1.0f / D) + 1e-5f);
+  rstd = rsqrtf(quad_group_sum(q) * (1.0f / D) + 1e-5f);
 }
 
 // LayerNorm of the wave's register-resident token block -> MFMA operands.
@@ -85,6 +81,7 @@ __device__ __forceinline__ void layer_norm(const float4_t (&res)[FB], const floa
                                            half8_t (&xn)[KS], int g) {
   float mean, rstd;
   row_stats(res, mean, rstd);
+  const float shift = -mean * rstd;
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
     float4_t lo, hi;
@@ -92,8 +89,8 @@ __device__ __forceinline__ void layer_norm(const float4_t (&res)[FB], const floa
     const float4_t b0 = ld4(beta + 32 * ks + 4 * g), b1 = ld4(beta + 32 * ks + 16 + 4 * g);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      lo[i] = (res[2 * ks][i] - mean) * rstd * g0[i] + b0[i];
-      hi[i] = (res[2 * ks + 1][i] - mean) * rstd * g1[i] + b1[i];
+      lo[i] = fmaf(fmaf(res[2 * ks][i], rstd, shift), g0[i], b0[i]);
+      hi[i] = fmaf(fmaf(res[2 * ks + 1][i], rstd, shift), g1[i], b1[i]);
     }
     xn[ks] = to_operand(lo, hi);
   }
@@ -286,9 +283,11 @@ __global__ __launch_bounds__(64 * NW, 1) void fused_stack_kernel(
           mx = fmaxf(mx, fmaxf(fmaxf(acc[0], acc[1]), fmaxf(acc[2], acc[3])));
         }
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      float lsum = 0.f;
+      mx = quad_group_max(mx);
+      // Row sums ride on the MFMA: an all-ones A operand gives sum_k P[q][k]
+      // in every row of the output block, i.e. in every lane of query q.
+      const half8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
+      float4_t lacc = {0.f, 0.f, 0.f, 0.f};
       const int vrow0 = HD < 16 ? 16 * (h / 2) : h * HD;
       float4_t o[HDB];
 #pragma unroll
@@ -302,8 +301,8 @@ __global__ __launch_bounds__(64 * NW, 1) void fused_stack_kernel(
             p0[i] = __builtin_amdgcn_exp2f(s[2 * kt][i] - mx);
             p1[i] = __builtin_amdgcn_exp2f(s[2 * kt + 1][i] - mx);  // exp2(-inf) = 0 past qb
           }
-          lsum += ((p0[0] + p0[1]) + (p0[2] + p0[3])) + ((p1[0] + p1[1]) + (p1[2] + p1[3]));
           const half8_t pf = to_operand(p0, p1);
+          lacc = mfma16x16x32(ones, pf, lacc);
 #pragma unroll
           for (int hb = 0; hb < HDB; ++hb) {
             const half_t* vr = vt_lds + (vrow0 + 16 * hb + r16) * LD + 32 * kt + 4 * g;
@@ -312,9 +311,7 @@ __global__ __launch_bounds__(64 * NW, 1) void fused_stack_kernel(
           }
         }
       }
-      lsum += __shfl_xor(lsum, 16);
-      lsum += __shfl_xor(lsum, 32);
-      const float inv = 1.0f / lsum;
+      const float inv = __builtin_amdgcn_rcpf(lacc[0]);
       // O^T C layout: lane holds features vrow0 + 16hb + 4g + i of query r16;
       // block 16c belongs to k-step c/2, half c&1 of the permuted operand.
       if constexpr (HD >= 16) {

@@ -224,7 +224,8 @@ def _gelu_as7126(x: np.ndarray) -> np.ndarray:
     t = 1.0 / (1.0 + p * z)
     poly = t * (a[0] + t * (a[1] + t * (a[2] + t * (a[3] + t * a[4]))))
     half_erfc = 0.5 * poly * np.exp(-z * z)
-    return x * np.where(x >= 0, 1.0 - half_erfc, half_erfc)
+    # x Phi(x) = max(x, 0) - |x| * 0.5 erfc(|x| / sqrt 2), the device's form
+    return np.maximum(x, 0.0) - np.abs(x) * half_erfc
 
 
 def test_gelu_approximation_error_bound():
