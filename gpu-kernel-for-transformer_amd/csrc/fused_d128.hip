@@ -72,7 +72,7 @@ __device__ __forceinline__ void row_stats(const float4_t (&r)[FB], float& mean, 
   for (int fb = 0; fb < FB; ++fb)
 #pragma unroll
     for (int i = 0; i < 4; ++i) { const float c = r[fb][i] - mean; q += c * c; }
-  rstd = rsqrtf(quad_group_sum(q) * (1.0f / D) + 1e-5f);
+  rstd = __builtin_amdgcn_rsqf(quad_group_sum(q) * (1.0f / D) + 1e-5f);  // argument >= 1e-5: no denormal path
 }
 
 // LayerNorm of the wave's register-resident token block -> MFMA operands.
@@ -117,6 +117,7 @@ __device__ __forceinline__ void drain_and_barrier() {
 constexpr int NW = 8;                  // waves per workgroup (two per SIMD)
 constexpr int F = 128;                 // ffn_dim (the packed-layer strides assume it)
 constexpr int FKS = F / 32;
+static_assert(F == D, "the staged-matrix GEMM assumes square 128 x 128 weights");
 constexpr int MATS = 6;                // Wq Wk Wv Wo W1 W2 per layer, each 128 x 128
 constexpr int MAT_FRAGS = D / 16 * KS; // 32 fragments of 16 x 32 halves (1 KB each)
 constexpr int MAT_BYTES = MAT_FRAGS * 1024;
@@ -129,6 +130,26 @@ static_assert(2 * D * 4 == NW * 8 * 16, "final LayerNorm vectors: 8 lanes x 16 b
 // Fragment `idx` of a staged matrix: 1 KB, lane-contiguous.
 __device__ __forceinline__ half8_t sfrag(const char* stage, int idx, int lane) {
   return *reinterpret_cast<const half8_t*>(stage + idx * 1024 + lane * 16);
+}
+
+// a[ob] += product of staged matrix block ob (16 outputs x 128 inputs) with
+// the register operands act, over all eight output blocks.  k-step outer:
+// the eight fragments of a k-step are read together and feed eight
+// independent MFMAs, so neither the LDS latency nor the MFMA dependency
+// latency is exposed per block.  SWAP: out^T = W . act^T (C layout: lane =
+// token, four features); otherwise out = act . W^T (lane = feature, four
+// tokens).
+template <bool SWAP>
+__device__ __forceinline__ void stage_gemm(const char* st, const half8_t (&act)[KS], float4_t (&a)[FB], int lane) {
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    half8_t f[FB];
+#pragma unroll
+    for (int ob = 0; ob < FB; ++ob) f[ob] = sfrag(st, ob * KS + ks, lane);
+#pragma unroll
+    for (int ob = 0; ob < FB; ++ob)
+      a[ob] = SWAP ? mfma16x16x32(f[ob], act[ks], a[ob]) : mfma16x16x32(act[ks], f[ob], a[ob]);
+  }
 }
 
 template <int HD>
@@ -208,38 +229,35 @@ __global__ __launch_bounds__(64 * NW, 1) void fused_stack_kernel(
       const char* st = begin_group(g0 + 0);
       float4_t qc[FB];
 #pragma unroll
-      for (int ob = 0; ob < FB; ++ob) {
-        float4_t a = ld4(pp + P_BQ + 16 * ob + 4 * g);  // Wq, bq carry scale * log2(e)
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) a = mfma16x16x32(sfrag(st, ob * KS + ks, lane), xn[ks], a);
-        qc[ob] = a;
-      }
+      for (int ob = 0; ob < FB; ++ob) qc[ob] = ld4(pp + P_BQ + 16 * ob + 4 * g);  // Wq, bq carry scale * log2(e)
+      stage_gemm<true>(st, xn, qc, lane);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) qop[ks] = to_operand(qc[2 * ks], qc[2 * ks + 1]);
     }
     // ---- K: LDS row-major, each k-step's 32 features in the permuted order --
     {
       const char* st = begin_group(g0 + 1);
+      float4_t a[FB];
 #pragma unroll
-      for (int ob = 0; ob < FB; ++ob) {
-        float4_t a = ld4(pp + P_BK + 16 * ob + 4 * g);
+      for (int ob = 0; ob < FB; ++ob) a[ob] = ld4(pp + P_BK + 16 * ob + 4 * g);
+      stage_gemm<true>(st, xn, a, lane);
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) a = mfma16x16x32(sfrag(st, ob * KS + ks, lane), xn[ks], a);
-        // features 32 (ob/2) + 16 (ob&1) + 4g + i sit at 32 (ob/2) + 8g + 4 (ob&1) + i
-        *reinterpret_cast<half4_t*>(k_lds + (16 * tb + r16) * LD + 32 * (ob / 2) + 8 * g + 4 * (ob & 1)) = to_half4(a);
-      }
+      for (int ob = 0; ob < FB; ++ob)  // features 32 (ob/2) + 16 (ob&1) + 4g + i sit at 32 (ob/2) + 8g + 4 (ob&1) + i
+        *reinterpret_cast<half4_t*>(k_lds + (16 * tb + r16) * LD + 32 * (ob / 2) + 8 * g + 4 * (ob & 1)) = to_half4(a[ob]);
     }
     // ---- V: unswapped product, lane = four consecutive entries of a V^T row --
     {
       const char* st = begin_group(g0 + 2);
+      float4_t a[FB];
 #pragma unroll
       for (int ob = 0; ob < FB; ++ob) {
         const float bv = pp[P_BV + 16 * ob + r16];
-        float4_t a = {bv, bv, bv, bv};
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) a = mfma16x16x32(xn[ks], sfrag(st, ob * KS + ks, lane), a);
-        *reinterpret_cast<half4_t*>(vt_lds + (16 * ob + r16) * LD + 16 * tb + 4 * g) = to_half4(a);
+        a[ob] = float4_t{bv, bv, bv, bv};
       }
+      stage_gemm<false>(st, xn, a, lane);
+#pragma unroll
+      for (int ob = 0; ob < FB; ++ob)
+        *reinterpret_cast<half4_t*>(vt_lds + (16 * ob + r16) * LD + 16 * tb + 4 * g) = to_half4(a[ob]);
     }
     __syncthreads();  // K and V^T of every token block are in LDS
 
@@ -336,13 +354,12 @@ __global__ __launch_bounds__(64 * NW, 1) void fused_stack_kernel(
     // ---- output projection + residual (Wo in permuted packing) ---------------
     {
       const char* st = begin_group(g0 + 3);
+      float4_t a[FB];
 #pragma unroll
-      for (int ob = 0; ob < FB; ++ob) {
-        float4_t a = {0.f, 0.f, 0.f, 0.f};
+      for (int ob = 0; ob < FB; ++ob) a[ob] = ld4(pp + P_BO + 16 * ob + 4 * g);
+      stage_gemm<true>(st, cop, a, lane);
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) a = mfma16x16x32(sfrag(st, ob * KS + ks, lane), cop[ks], a);
-        res[ob] += a + ld4(pp + P_BO + 16 * ob + 4 * g);
-      }
+      for (int ob = 0; ob < FB; ++ob) res[ob] += a[ob];
     }
 
     // ---- LN2, FFN: gelu(n2 W1^T + b1) W2^T + b2 + residual ----------------
@@ -350,24 +367,23 @@ __global__ __launch_bounds__(64 * NW, 1) void fused_stack_kernel(
     half8_t hf[FKS];
     {
       const char* st = begin_group(g0 + 4);
+      float4_t a[FB];
 #pragma unroll
-      for (int ob = 0; ob < 2 * FKS; ++ob) {
-        float4_t a = ld4(pp + P_B1 + 16 * ob + 4 * g);
+      for (int ob = 0; ob < FB; ++ob) a[ob] = ld4(pp + P_B1 + 16 * ob + 4 * g);
+      stage_gemm<true>(st, xn, a, lane);
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) a = mfma16x16x32(sfrag(st, ob * KS + ks, lane), xn[ks], a);
+      for (int ob = 0; ob < FB; ++ob)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) hf[ob / 2][(ob & 1) * 4 + i] = (half_t)gelu_erf(a[i]);
-      }
+        for (int i = 0; i < 4; ++i) hf[ob / 2][(ob & 1) * 4 + i] = (half_t)gelu_erf(a[ob][i]);
     }
     {
       const char* st = begin_group(g0 + 5);
+      float4_t a[FB];
 #pragma unroll
-      for (int ob = 0; ob < FB; ++ob) {
-        float4_t a = {0.f, 0.f, 0.f, 0.f};
+      for (int ob = 0; ob < FB; ++ob) a[ob] = ld4(pp + P_B2 + 16 * ob + 4 * g);
+      stage_gemm<true>(st, hf, a, lane);
 #pragma unroll
-        for (int ks = 0; ks < FKS; ++ks) a = mfma16x16x32(sfrag(st, ob * FKS + ks, lane), hf[ks], a);
-        res[ob] += a + ld4(pp + P_B2 + 16 * ob + 4 * g);
-      }
+      for (int ob = 0; ob < FB; ++ob) res[ob] += a[ob];
     }
   }
 
