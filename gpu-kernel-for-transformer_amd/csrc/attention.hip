@@ -27,11 +27,13 @@
 // V[32t + 4g + j/4][16hb + 4(j%4)].
 //
 // Softmax is online in FP32, base 2, with Q pre-multiplied by scale*log2(e).
-// The row sum comes out of the MFMA as one extra O^T block whose V^T rows are
-// all ones, and the running maximum is only moved (and O rescaled) when a
-// tile's maximum exceeds it by more than 8 (probabilities then stay <= 2^8,
-// exact enough in FP16); the decision is wave-uniform.  Only tiles that
-// straddle the diagonal pay for the mask.
+// The score MFMAs accumulate onto -m_run (the running exponent offset), so
+// the probabilities are a bare exp2 of the accumulator.  The row sum comes out
+// of the MFMA as one extra O^T block whose V^T rows are all ones, and m_run is
+// only moved (and O rescaled) on the first tile and when a tile's maximum
+// exceeds it by more than 8 (probabilities then stay <= 2^8, exact enough in
+// FP16); the decision is wave-uniform.  Only tiles that straddle the diagonal
+// pay for the mask.
 #include "common.h"
 #include "../../include/xblock.h"
 
@@ -45,7 +47,10 @@ struct AttnCfg {
   static constexpr int QPW = 16 * NQ;                 // queries per wave
   static constexpr int BQ = 4 * QPW;                  // queries per block
   static constexpr int LDK = HDP + 8;                 // K tile row stride (halves)
-  static constexpr int LDV = HDV + 8;                 // V tile row stride (halves)
+  // V tile row stride (halves): a multiple of 16 halves with an odd quotient
+  // (row stride an odd multiple of 32 bytes), which spreads the 32 rows x 8
+  // bytes one half-wave of ds_read_b64_tr_b16 touches over all 64 banks.
+  static constexpr int LDV = (HDV / 16) % 2 ? HDV : HDV + 16;
   static constexpr int KSTEPS = HDP / 32, KB = BKEYS / 16, HB = HDV / 16, KT = BKEYS / 32;
   static constexpr int CPK = HD / 8;                  // 16-byte chunks per key row
   static constexpr int CH = (BKEYS * CPK + 255) / 256;  // chunks per thread per tile
@@ -120,6 +125,9 @@ __global__ __launch_bounds__(256, 2) void attn_causal_kernel(
     }
   }
 
+  // m_run: the base-2 exponent offset of query (l % 16) of block qb.  The score
+  // MFMAs start from -m_run, so a tile's scores arrive already shifted; the
+  // first tile moves m_run onto its exact maximum.
   float4_t o[HB][NQ], lacc[NQ];
   float m_run[NQ];
 #pragma unroll
@@ -127,7 +135,7 @@ __global__ __launch_bounds__(256, 2) void attn_causal_kernel(
 #pragma unroll
     for (int hb = 0; hb < HB; ++hb) o[hb][qb] = float4_t{0.f, 0.f, 0.f, 0.f};
     lacc[qb] = float4_t{0.f, 0.f, 0.f, 0.f};
-    m_run[qb] = -INFINITY;
+    m_run[qb] = 0.f;
   }
   const half8_t ones8 = {1, 1, 1, 1, 1, 1, 1, 1};
 
@@ -175,12 +183,16 @@ __global__ __launch_bounds__(256, 2) void attn_causal_kernel(
       const half_t* kt_lds = k_lds[cur];
       const half_t* vt_lds = v_lds[cur];
 
-      // S^T tile = K . Q^T  ->  s[jb][qb][i]: key k0+16jb+4g+i, query qw0+16qb+r16
+      // S^T tile = K . Q^T - m_run  ->  s[jb][qb][i]: key k0+16jb+4g+i, query qw0+16qb+r16
       float4_t s[KB][NQ];
+      // Wave priority: raised over the MFMA-heavy stretches (the score MFMAs,
+      // then the exp + PV MFMA interleave), normal over the max / rescale and
+      // the tile store, so the co-resident wave's VALU work fills the gaps.
+      __builtin_amdgcn_s_setprio(3);
 #pragma unroll
       for (int jb = 0; jb < KB; ++jb) {
 #pragma unroll
-        for (int qb = 0; qb < NQ; ++qb) s[jb][qb] = float4_t{0.f, 0.f, 0.f, 0.f};
+        for (int qb = 0; qb < NQ; ++qb) s[jb][qb] = float4_t{-m_run[qb], -m_run[qb], -m_run[qb], -m_run[qb]};
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) {
           const half8_t kf = *reinterpret_cast<const half8_t*>(kt_lds + (16 * jb + r16) * LDK + 32 * ks + 8 * g);
@@ -188,6 +200,7 @@ __global__ __launch_bounds__(256, 2) void attn_causal_kernel(
           for (int qb = 0; qb < NQ; ++qb) s[jb][qb] = mfma16x16x32(kf, qf[qb][ks], s[jb][qb]);
         }
       }
+      __builtin_amdgcn_s_setprio(0);
       if (diag) {
 #pragma unroll
         for (int jb = 0; jb < KB; ++jb)
@@ -198,32 +211,37 @@ __global__ __launch_bounds__(256, 2) void attn_causal_kernel(
               if (k0 + 16 * jb + 4 * g + i > qw0 + 16 * qb + r16) s[jb][qb][i] = -INFINITY;
       }
 
-      // Tile maximum per query; move the running maximum only when it grew by > 8.
-      float mx[NQ];
-      bool grow = false;
+      // The offset moves onto the exact per-query maximum on the first tile,
+      // and afterwards only when some score exceeds it by more than 8
+      // (probabilities then stay <= 2^8, exact enough in FP16).  Whether any
+      // does is a lane-local max and one wave vote; the per-query maxima are
+      // only formed on that rare path.
+      float lm = -INFINITY;
 #pragma unroll
-      for (int qb = 0; qb < NQ; ++qb) {
-        float m = -INFINITY;
+      for (int qb = 0; qb < NQ; ++qb)
 #pragma unroll
         for (int jb = 0; jb < KB; ++jb)
-          m = fmaxf(m, fmaxf(fmaxf(s[jb][qb][0], s[jb][qb][1]), fmaxf(s[jb][qb][2], s[jb][qb][3])));
-        m = fmaxf(m, __shfl_xor(m, 16));
-        m = fmaxf(m, __shfl_xor(m, 32));
-        mx[qb] = m;
-        grow |= m > m_run[qb] + 8.0f;
-      }
-      if (__any(grow)) {
+          lm = fmaxf(lm, fmaxf(fmaxf(s[jb][qb][0], s[jb][qb][1]), fmaxf(s[jb][qb][2], s[jb][qb][3])));
+      if (__any(t == 0 || lm > 8.0f)) {
 #pragma unroll
         for (int qb = 0; qb < NQ; ++qb) {
-          const float m_new = fmaxf(m_run[qb], mx[qb]);
-          const float corr = __builtin_amdgcn_exp2f(m_run[qb] - m_new);
-          m_run[qb] = m_new;
+          float m = -INFINITY;
+#pragma unroll
+          for (int jb = 0; jb < KB; ++jb)
+            m = fmaxf(m, fmaxf(fmaxf(s[jb][qb][0], s[jb][qb][1]), fmaxf(s[jb][qb][2], s[jb][qb][3])));
+          const float mx = quad_group_max(m);
+          const float sh = t == 0 ? mx : fmaxf(mx, 0.f);
+          const float corr = __builtin_amdgcn_exp2f(-sh);
+          m_run[qb] += sh;
 #pragma unroll
           for (int hb = 0; hb < HB; ++hb) o[hb][qb] *= corr;
           lacc[qb] *= corr;
+#pragma unroll
+          for (int jb = 0; jb < KB; ++jb) s[jb][qb] -= sh;
         }
       }
 
+      __builtin_amdgcn_s_setprio(3);
       // O^T += V^T . P^T (and the row sums via an all-ones V^T block), 32 keys per step.
 #pragma unroll
       for (int kt = 0; kt < KT; ++kt) {
@@ -232,8 +250,8 @@ __global__ __launch_bounds__(256, 2) void attn_causal_kernel(
         for (int qb = 0; qb < NQ; ++qb)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            pf[qb][i] = (half_t)__builtin_amdgcn_exp2f(s[2 * kt][qb][i] - m_run[qb]);
-            pf[qb][4 + i] = (half_t)__builtin_amdgcn_exp2f(s[2 * kt + 1][qb][i] - m_run[qb]);
+            pf[qb][i] = (half_t)__builtin_amdgcn_exp2f(s[2 * kt][qb][i]);
+            pf[qb][4 + i] = (half_t)__builtin_amdgcn_exp2f(s[2 * kt + 1][qb][i]);
           }
 #pragma unroll
         for (int qb = 0; qb < NQ; ++qb) lacc[qb] = mfma16x16x32(ones8, pf[qb], lacc[qb]);
@@ -249,6 +267,7 @@ __global__ __launch_bounds__(256, 2) void attn_causal_kernel(
       }
     }
 
+    __builtin_amdgcn_s_setprio(0);
     if (t + 1 < n_tiles) sstore(cur ^ 1);
     __syncthreads();
   }
@@ -258,7 +277,7 @@ __global__ __launch_bounds__(256, 2) void attn_causal_kernel(
   half_t* obase = out + (int64_t)b * S * D + (int64_t)h * HD;
 #pragma unroll
   for (int qb = 0; qb < NQ; ++qb) {
-    const float inv = 1.0f / lacc[qb][0];
+    const float inv = __builtin_amdgcn_rcpf(lacc[qb][0]);
     const int q = qw0 + 16 * qb + r16;
     if (q >= S) continue;
 #pragma unroll
