@@ -19,7 +19,7 @@ from .config import (
     TransformerConfig,
     resolve_shape_execution_plan,
 )
-from .kernels import causal_attention, ffn_gelu, fused_residual_layer_norm, layer_norm, linear
+from .kernels import attention, causal_attention, ffn_gelu, fused_residual_layer_norm, layer_norm, linear
 from .model import (
     SelfAttentionParameters,
     TransformerBlockParameters,
@@ -39,6 +39,7 @@ __all__ = [
     "UserOptimizedTransformer",
     "XBLOCK_AVAILABLE",
     "XBLOCK_LOAD_ERROR",
+    "attention",
     "causal_attention",
     "ffn_gelu",
     "forward_bytes",

@@ -32,14 +32,19 @@ XB_EPI_BIAS = 0
 XB_EPI_BIAS_GELU = 1
 XB_PACK_PERMUTED = 0
 XB_PACK_NATURAL = 1
+XB_MASK_UPDATE = 1
+XB_MASK_SUM = 2
+XB_MASK_OUTPUT = 4
 
 EXPORTED_SYMBOLS = (
     "xb_abi_version",
     "xb_strerror",
     "xb_layernorm",
     "xb_residual_layernorm",
+    "xb_residual_layernorm_masked",
     "xb_linear",
     "xb_attention_causal",
+    "xb_attention",
     "xb_pack_linear_fragments",
     "xb_fused_forward_d128",
 )
@@ -56,8 +61,14 @@ _SIGNATURES = {
         ctypes.c_int,
         [_vp, _vp, ctypes.c_int, _vp, _vp, _vp, _vp, ctypes.c_int, _i64, _i32, _f32, ctypes.c_int, _vp],
     ),
+    "xb_residual_layernorm_masked": (
+        ctypes.c_int,
+        [_vp, _vp, ctypes.c_int, _vp, _vp, _vp, _vp, ctypes.c_int, _i64, _i32, _f32, ctypes.c_int,
+         _vp, ctypes.c_int, _vp],
+    ),
     "xb_linear": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, ctypes.c_int, _vp]),
     "xb_attention_causal": (ctypes.c_int, [_vp, _vp, _i32, _i64, _i32, _i32, _f32, _vp]),
+    "xb_attention": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i64, _i32, _i32, _f32, _i32, _vp]),
     "xb_pack_linear_fragments": (ctypes.c_int, [_vp, _vp, _i32, _i32, _i32, _f32, _vp]),
     "xb_fused_forward_d128": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp]),
 }

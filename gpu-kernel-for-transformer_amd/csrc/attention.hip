@@ -64,10 +64,15 @@ __device__ __forceinline__ half4_t lds_read_tr16(const half_t* p) {
   return __builtin_bit_cast(half4_t, v);
 }
 
-template <int HD, int NQ>
-__global__ __launch_bounds__(256, 2) void attn_causal_kernel(
-    const half_t* __restrict__ qkv, half_t* __restrict__ out, int H, int S,
-    int q_tiles, float scale_log2) {
+// CAUSAL: apply the top-left causal mask.  KEYMASK: key_valid ([B, S] bytes,
+// nonzero = the key may be attended to -- the reference's valid_token_mask,
+// TTB:250-253) is staged per tile and masks keys; a query may then see no key
+// in a tile, or at all.  Without KEYMASK every query sees key 0 in the first
+// tile, which keeps the offset bookkeeping to a tile-index test.
+template <int HD, int NQ, bool CAUSAL, bool KEYMASK>
+__global__ __launch_bounds__(256, 2) void attn_kernel(
+    const half_t* __restrict__ qkv, half_t* __restrict__ out, const uint8_t* __restrict__ key_valid,
+    int H, int S, int q_tiles, float scale_log2) {
   using C = AttnCfg<HD, NQ>;
   constexpr int BKEYS = C::BKEYS, HDP = C::HDP, HDV = C::HDV, QPW = C::QPW, BQ = C::BQ;
   constexpr int LDK = C::LDK, LDV = C::LDV, KSTEPS = C::KSTEPS, KB = C::KB, HB = C::HB;
@@ -75,10 +80,11 @@ __global__ __launch_bounds__(256, 2) void attn_causal_kernel(
 
   __shared__ __attribute__((aligned(16))) half_t k_lds[2][BKEYS * LDK];
   __shared__ __attribute__((aligned(16))) half_t v_lds[2][BKEYS * LDV];
+  __shared__ __attribute__((aligned(16))) uint8_t kv_lds[2][BKEYS];  // key validity of the tile
 
   // Heaviest query tiles (most keys under the causal mask) are issued first.
   const int bh = blockIdx.x / q_tiles;
-  const int qt = q_tiles - 1 - (blockIdx.x % q_tiles);
+  const int qt = CAUSAL ? q_tiles - 1 - (blockIdx.x % q_tiles) : blockIdx.x % q_tiles;
   const int b = bh / H, h = bh % H;
   const int D = H * HD;
   const int64_t row_stride = 3 * (int64_t)D;  // halves between consecutive tokens
@@ -127,20 +133,31 @@ __global__ __launch_bounds__(256, 2) void attn_causal_kernel(
 
   // m_run: the base-2 exponent offset of query (l % 16) of block qb.  The score
   // MFMAs start from -m_run, so a tile's scores arrive already shifted; the
-  // first tile moves m_run onto its exact maximum.
+  // first tile with a visible key for a query moves m_run onto that tile's
+  // exact maximum (m_set records that it happened; without KEYMASK that is
+  // always tile 0).
   float4_t o[HB][NQ], lacc[NQ];
   float m_run[NQ];
+  bool m_set[NQ];
 #pragma unroll
   for (int qb = 0; qb < NQ; ++qb) {
 #pragma unroll
     for (int hb = 0; hb < HB; ++hb) o[hb][qb] = float4_t{0.f, 0.f, 0.f, 0.f};
     lacc[qb] = float4_t{0.f, 0.f, 0.f, 0.f};
     m_run[qb] = 0.f;
+    m_set[qb] = false;
   }
   const half8_t ones8 = {1, 1, 1, 1, 1, 1, 1, 1};
 
+  // Key validity travels with the tile (0 past S as well).
+  const uint8_t* kvb = KEYMASK ? key_valid + (int64_t)b * S : nullptr;
+  uint8_t kvreg = 0;
   half8_t kreg[CH], vreg[CH];
   auto gload = [&](int k0) {
+    if (KEYMASK && tid < BKEYS) {
+      const int key = k0 + tid;
+      kvreg = key < S ? kvb[key] : (uint8_t)0;
+    }
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
       const int id = tid + 256 * j;
@@ -156,6 +173,7 @@ __global__ __launch_bounds__(256, 2) void attn_causal_kernel(
     }
   };
   auto sstore = [&](int buf) {
+    if (KEYMASK && tid < BKEYS) kv_lds[buf][tid] = kvreg;
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
       const int id = tid + 256 * j;
@@ -167,7 +185,7 @@ __global__ __launch_bounds__(256, 2) void attn_causal_kernel(
     }
   };
 
-  const int key_end = min(S, q0 + BQ);
+  const int key_end = CAUSAL ? min(S, q0 + BQ) : S;
   const int n_tiles = (key_end + BKEYS - 1) / BKEYS;
   gload(0);
   sstore(0);
@@ -178,8 +196,9 @@ __global__ __launch_bounds__(256, 2) void attn_causal_kernel(
     if (t + 1 < n_tiles) gload(k0 + BKEYS);
 
     // Wave-uniform skip: every key of this tile lies above this wave's diagonal.
-    if (k0 <= qw0 + QPW - 1) {
-      const bool diag = (k0 + BKEYS - 1 > qw0);
+    if (!CAUSAL || k0 <= qw0 + QPW - 1) {
+      const bool diag = CAUSAL && (k0 + BKEYS - 1 > qw0);
+      // Non-causal tiles that run past S mask those keys (causal ones already do).
       const half_t* kt_lds = k_lds[cur];
       const half_t* vt_lds = v_lds[cur];
 
@@ -210,19 +229,41 @@ __global__ __launch_bounds__(256, 2) void attn_causal_kernel(
             for (int i = 0; i < 4; ++i)
               if (k0 + 16 * jb + 4 * g + i > qw0 + 16 * qb + r16) s[jb][qb][i] = -INFINITY;
       }
-
-      // The offset moves onto the exact per-query maximum on the first tile,
-      // and afterwards only when some score exceeds it by more than 8
-      // (probabilities then stay <= 2^8, exact enough in FP16).  Whether any
-      // does is a lane-local max and one wave vote; the per-query maxima are
-      // only formed on that rare path.
-      float lm = -INFINITY;
+      if constexpr (KEYMASK) {
 #pragma unroll
-      for (int qb = 0; qb < NQ; ++qb)
+        for (int jb = 0; jb < KB; ++jb) {
+          const uint32_t v4 = *reinterpret_cast<const uint32_t*>(&kv_lds[cur][16 * jb + 4 * g]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (((v4 >> (8 * i)) & 0xffu) == 0u)
+#pragma unroll
+              for (int qb = 0; qb < NQ; ++qb) s[jb][qb][i] = -INFINITY;
+        }
+      } else if (!CAUSAL && k0 + BKEYS > S) {
+#pragma unroll
+        for (int jb = 0; jb < KB; ++jb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (k0 + 16 * jb + 4 * g + i >= S)
+#pragma unroll
+              for (int qb = 0; qb < NQ; ++qb) s[jb][qb][i] = -INFINITY;
+      }
+
+      // The offset moves onto the exact per-query maximum on the first tile
+      // that shows the query a key, and afterwards only when some score
+      // exceeds it by more than 8 (probabilities then stay <= 2^8, exact
+      // enough in FP16).  Whether any does is a lane-local max and one wave
+      // vote; the per-query maxima are only formed on that rare path.
+      float lm = -INFINITY;
+      bool unset = t == 0;
+#pragma unroll
+      for (int qb = 0; qb < NQ; ++qb) {
+        if constexpr (KEYMASK) unset |= !m_set[qb];
 #pragma unroll
         for (int jb = 0; jb < KB; ++jb)
           lm = fmaxf(lm, fmaxf(fmaxf(s[jb][qb][0], s[jb][qb][1]), fmaxf(s[jb][qb][2], s[jb][qb][3])));
-      if (__any(t == 0 || lm > 8.0f)) {
+      }
+      if (__any(unset || lm > 8.0f)) {
 #pragma unroll
         for (int qb = 0; qb < NQ; ++qb) {
           float m = -INFINITY;
@@ -230,8 +271,13 @@ __global__ __launch_bounds__(256, 2) void attn_causal_kernel(
           for (int jb = 0; jb < KB; ++jb)
             m = fmaxf(m, fmaxf(fmaxf(s[jb][qb][0], s[jb][qb][1]), fmaxf(s[jb][qb][2], s[jb][qb][3])));
           const float mx = quad_group_max(m);
-          const float sh = t == 0 ? mx : fmaxf(mx, 0.f);
-          const float corr = __builtin_amdgcn_exp2f(-sh);
+          // Until a query has seen a key its o and lacc are exactly zero: the
+          // offset jumps to the first finite maximum and nothing is rescaled
+          // (exp2(-sh) could overflow there).  Afterwards sh >= 0, corr <= 1.
+          const bool was_set = KEYMASK ? m_set[qb] : t != 0;
+          const float sh = was_set ? fmaxf(mx, 0.f) : (KEYMASK && mx == -INFINITY ? 0.f : mx);
+          if constexpr (KEYMASK) m_set[qb] = was_set || mx != -INFINITY;
+          const float corr = was_set ? __builtin_amdgcn_exp2f(-sh) : 1.f;
           m_run[qb] += sh;
 #pragma unroll
           for (int hb = 0; hb < HB; ++hb) o[hb][qb] *= corr;
@@ -277,7 +323,8 @@ __global__ __launch_bounds__(256, 2) void attn_causal_kernel(
   half_t* obase = out + (int64_t)b * S * D + (int64_t)h * HD;
 #pragma unroll
   for (int qb = 0; qb < NQ; ++qb) {
-    const float inv = __builtin_amdgcn_rcpf(lacc[qb][0]);
+    // A query that saw no key at all (every key masked) writes zeros.
+    const float inv = lacc[qb][0] > 0.f ? __builtin_amdgcn_rcpf(lacc[qb][0]) : 0.f;
     const int q = qw0 + 16 * qb + r16;
     if (q >= S) continue;
 #pragma unroll
@@ -294,30 +341,40 @@ __global__ __launch_bounds__(256, 2) void attn_causal_kernel(
 }
 
 template <int HD, int NQ>
-static hipError_t launch_attn(const half_t* qkv, half_t* out, int B, int S, int H, float scale,
-                              hipStream_t s) {
+static hipError_t launch_attn(const half_t* qkv, half_t* out, const uint8_t* kv, int B, int S, int H,
+                              float scale, int causal, hipStream_t s) {
   constexpr int BQ = AttnCfg<HD, NQ>::BQ;
   const int q_tiles = (S + BQ - 1) / BQ;
   const int64_t blocks = (int64_t)q_tiles * B * H;
   if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
   const float scale_log2 = scale * 1.44269504088896340736f;
-  hipLaunchKernelGGL((attn_causal_kernel<HD, NQ>), dim3((unsigned)blocks), dim3(256), 0, s, qkv, out,
-                     H, S, q_tiles, scale_log2);
+  const dim3 grid((unsigned)blocks);
+  if (kv != nullptr) {
+    if (causal)
+      hipLaunchKernelGGL((attn_kernel<HD, NQ, true, true>), grid, dim3(256), 0, s, qkv, out, kv, H, S, q_tiles, scale_log2);
+    else
+      hipLaunchKernelGGL((attn_kernel<HD, NQ, false, true>), grid, dim3(256), 0, s, qkv, out, kv, H, S, q_tiles, scale_log2);
+  } else {
+    if (causal)
+      hipLaunchKernelGGL((attn_kernel<HD, NQ, true, false>), grid, dim3(256), 0, s, qkv, out, kv, H, S, q_tiles, scale_log2);
+    else
+      hipLaunchKernelGGL((attn_kernel<HD, NQ, false, false>), grid, dim3(256), 0, s, qkv, out, kv, H, S, q_tiles, scale_log2);
+  }
   return hipGetLastError();
 }
 
 // Long sequences take 64 queries per wave (each K/V fragment read from LDS
 // then feeds 4 MFMAs); short ones keep 32 so a block does not outgrow S.
 template <int HD>
-static hipError_t dispatch_attn(const half_t* qkv, half_t* out, int B, int S, int H, float scale,
-                                hipStream_t s) {
+static hipError_t dispatch_attn(const half_t* qkv, half_t* out, const uint8_t* kv, int B, int S, int H,
+                                float scale, int causal, hipStream_t s) {
   if constexpr (HD >= 256) {
-    return launch_attn<HD, 1>(qkv, out, B, S, H, scale, s);
+    return launch_attn<HD, 1>(qkv, out, kv, B, S, H, scale, causal, s);
   } else if constexpr (HD >= 128) {
-    return launch_attn<HD, 2>(qkv, out, B, S, H, scale, s);
+    return launch_attn<HD, 2>(qkv, out, kv, B, S, H, scale, causal, s);
   } else {
-    if (S >= 1024) return launch_attn<HD, 4>(qkv, out, B, S, H, scale, s);
-    return launch_attn<HD, 2>(qkv, out, B, S, H, scale, s);
+    if (S >= 1024) return launch_attn<HD, 4>(qkv, out, kv, B, S, H, scale, causal, s);
+    return launch_attn<HD, 2>(qkv, out, kv, B, S, H, scale, causal, s);
   }
 }
 
@@ -325,8 +382,9 @@ static hipError_t dispatch_attn(const half_t* qkv, half_t* out, int B, int S, in
 
 using namespace xb;
 
-extern "C" int xb_attention_causal(const void* qkv, void* out, int32_t batch, int64_t seq_len,
-                                   int32_t heads, int32_t head_dim, float scale, void* stream) {
+extern "C" int xb_attention(const void* qkv, void* out, const uint8_t* key_valid, int32_t batch,
+                            int64_t seq_len, int32_t heads, int32_t head_dim, float scale, int32_t causal,
+                            void* stream) {
   if (batch < 0 || seq_len < 0 || heads <= 0 || head_dim <= 0) return XB_ERR_BAD_SIZE;
   if (seq_len > 0x7fffffffLL / 4) return XB_ERR_BAD_SIZE;
   if (head_dim != 8 && head_dim != 16 && head_dim != 32 && head_dim != 64 && head_dim != 128 &&
@@ -339,14 +397,20 @@ extern "C" int xb_attention_causal(const void* qkv, void* out, int32_t batch, in
   const half_t* q = static_cast<const half_t*>(qkv);
   half_t* o = static_cast<half_t*>(out);
   const int S = (int)seq_len;
+  const int c = causal ? 1 : 0;
   hipError_t e;
   switch (head_dim) {
-    case 8: e = dispatch_attn<8>(q, o, batch, S, heads, scale, s); break;
-    case 16: e = dispatch_attn<16>(q, o, batch, S, heads, scale, s); break;
-    case 32: e = dispatch_attn<32>(q, o, batch, S, heads, scale, s); break;
-    case 64: e = dispatch_attn<64>(q, o, batch, S, heads, scale, s); break;
-    case 128: e = dispatch_attn<128>(q, o, batch, S, heads, scale, s); break;
-    default: e = dispatch_attn<256>(q, o, batch, S, heads, scale, s); break;
+    case 8: e = dispatch_attn<8>(q, o, key_valid, batch, S, heads, scale, c, s); break;
+    case 16: e = dispatch_attn<16>(q, o, key_valid, batch, S, heads, scale, c, s); break;
+    case 32: e = dispatch_attn<32>(q, o, key_valid, batch, S, heads, scale, c, s); break;
+    case 64: e = dispatch_attn<64>(q, o, key_valid, batch, S, heads, scale, c, s); break;
+    case 128: e = dispatch_attn<128>(q, o, key_valid, batch, S, heads, scale, c, s); break;
+    default: e = dispatch_attn<256>(q, o, key_valid, batch, S, heads, scale, c, s); break;
   }
   return (int)e;
+}
+
+extern "C" int xb_attention_causal(const void* qkv, void* out, int32_t batch, int64_t seq_len,
+                                   int32_t heads, int32_t head_dim, float scale, void* stream) {
+  return xb_attention(qkv, out, nullptr, batch, seq_len, heads, head_dim, scale, 1, stream);
 }

@@ -48,11 +48,16 @@ struct Vec8<half_t> {
 
 // D = CH * LPR * 8 columns; 256 / LPR rows per 256-thread block.
 // RES: add `upd` to `x` first and (when res_out != nullptr) store the sum.
+// row_valid (optional, one byte per row) with mask_mode bits
+// XB_MASK_UPDATE / XB_MASK_SUM / XB_MASK_OUTPUT zeroes, for rows whose byte
+// is 0, the update, the sum (stored residual and LayerNorm input), or the
+// output (by selection, so NaN in a masked update does not leak).
 template <int D, int LPR, bool RES, typename TU, typename TY>
 __global__ __launch_bounds__(256) void ln_rows_kernel(
     const float* x, const TU* __restrict__ upd,
     const float* __restrict__ gamma, const float* __restrict__ beta,
-    float* res_out, TY* __restrict__ y, int64_t rows, float eps, int affine) {
+    float* res_out, TY* __restrict__ y, int64_t rows, float eps, int affine,
+    const uint8_t* __restrict__ row_valid, int mask_mode) {
   constexpr int CH = D / (LPR * 8);
   static_assert(CH * LPR * 8 == D, "row width must split into 8-column lanes");
   constexpr int RPB = 256 / LPR;
@@ -61,6 +66,10 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(
   // Every lane of a row group takes the same branch, so the width-LPR
   // shuffles below only ever read lanes that are still active.
   if (row >= rows) return;
+  const bool invalid = row_valid != nullptr && row_valid[row] == 0;
+  const bool drop_update = invalid && (mask_mode & XB_MASK_UPDATE);
+  const bool drop_sum = invalid && (mask_mode & XB_MASK_SUM);
+  const bool drop_out = invalid && (mask_mode & XB_MASK_OUTPUT);
 
   float v[CH][8];
   const float* xr = x + row * D;
@@ -69,10 +78,16 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(
     const int col = (c * LPR + lr) * 8;
     Vec8<float>::load(xr + col, v[c]);
     if constexpr (RES) {
-      float u[8];
-      Vec8<TU>::load(upd + row * D + col, u);
+      if (!drop_update) {
+        float u[8];
+        Vec8<TU>::load(upd + row * D + col, u);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[c][i] += u[i];
+        for (int i = 0; i < 8; ++i) v[c][i] += u[i];
+      }
+    }
+    if (drop_sum) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[c][i] = 0.f;
     }
   }
   if constexpr (RES) {
@@ -112,6 +127,10 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(
 #pragma unroll
       for (int i = 0; i < 8; ++i) o[i] = v[c][i] * rstd;
     }
+    if (drop_out) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = 0.f;
+    }
     Vec8<TY>::store(y + row * D + col, o);
   }
 }
@@ -121,18 +140,26 @@ template <bool RES, typename TU, typename TY>
 __global__ __launch_bounds__(256) void ln_generic_kernel(
     const float* x, const TU* __restrict__ upd,
     const float* __restrict__ gamma, const float* __restrict__ beta,
-    float* res_out, TY* __restrict__ y, int cols, float eps, int affine) {
+    float* res_out, TY* __restrict__ y, int cols, float eps, int affine,
+    const uint8_t* __restrict__ row_valid, int mask_mode) {
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
   const float* xr = x + row * cols;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const bool invalid = row_valid != nullptr && row_valid[row] == 0;
+  const bool drop_update = invalid && (mask_mode & XB_MASK_UPDATE);
+  const bool drop_sum = invalid && (mask_mode & XB_MASK_SUM);
+  const bool drop_out = invalid && (mask_mode & XB_MASK_OUTPUT);
 
   float s = 0.f;
   for (int c = threadIdx.x; c < cols; c += 256) {
     float v = xr[c];
     if constexpr (RES) {
-      v += (float)upd[row * cols + c];
+      if (!drop_update) v += (float)upd[row * cols + c];
+      if (drop_sum) v = 0.f;
       if (res_out != nullptr) res_out[row * cols + c] = v;
+    } else {
+      if (drop_sum) v = 0.f;
     }
     s += v;
   }
@@ -145,9 +172,10 @@ __global__ __launch_bounds__(256) void ln_generic_kernel(
   // Later passes re-read the summed row; when res_out is set (possibly
   // aliasing x) it already holds the sum this thread wrote in pass one.
   auto summed = [&](int c) -> float {
+    if (drop_sum) return 0.f;
     if constexpr (RES) {
       if (res_out != nullptr) return res_out[row * cols + c];
-      return xr[c] + (float)upd[row * cols + c];
+      return drop_update ? xr[c] : xr[c] + (float)upd[row * cols + c];
     } else {
       return xr[c];
     }
@@ -165,6 +193,7 @@ __global__ __launch_bounds__(256) void ln_generic_kernel(
   for (int c = threadIdx.x; c < cols; c += 256) {
     float o = (summed(c) - mean) * rstd;
     if (affine) o = o * gamma[c] + beta[c];
+    if (drop_out) o = 0.f;
     y[row * cols + c] = (TY)o;
   }
 }
@@ -173,12 +202,12 @@ template <int D, int LPR, bool RES, typename TU, typename TY>
 static hipError_t launch_rows(const float* x, const void* upd, const float* g,
                               const float* b, float* res_out, void* y,
                               int64_t rows, float eps, int affine,
-                              hipStream_t s) {
+                              const uint8_t* rv, int mm, hipStream_t s) {
   constexpr int RPB = 256 / LPR;
   const int64_t blocks = (rows + RPB - 1) / RPB;
   hipLaunchKernelGGL((ln_rows_kernel<D, LPR, RES, TU, TY>), dim3((unsigned)blocks),
                      dim3(256), 0, s, x, static_cast<const TU*>(upd), g, b,
-                     res_out, static_cast<TY*>(y), rows, eps, affine);
+                     res_out, static_cast<TY*>(y), rows, eps, affine, rv, mm);
   return hipGetLastError();
 }
 
@@ -186,18 +215,18 @@ template <bool RES, typename TU, typename TY>
 static hipError_t dispatch_width(const float* x, const void* upd, const float* g,
                                  const float* b, float* res_out, void* y,
                                  int64_t rows, int cols, float eps, int affine,
-                                 hipStream_t s) {
+                                 hipStream_t s, const uint8_t* rv = nullptr, int mm = 0) {
   switch (cols) {
-    case 64: return launch_rows<64, 8, RES, TU, TY>(x, upd, g, b, res_out, y, rows, eps, affine, s);
-    case 128: return launch_rows<128, 16, RES, TU, TY>(x, upd, g, b, res_out, y, rows, eps, affine, s);
-    case 256: return launch_rows<256, 32, RES, TU, TY>(x, upd, g, b, res_out, y, rows, eps, affine, s);
-    case 512: return launch_rows<512, 64, RES, TU, TY>(x, upd, g, b, res_out, y, rows, eps, affine, s);
-    case 1024: return launch_rows<1024, 64, RES, TU, TY>(x, upd, g, b, res_out, y, rows, eps, affine, s);
-    case 2048: return launch_rows<2048, 64, RES, TU, TY>(x, upd, g, b, res_out, y, rows, eps, affine, s);
+    case 64: return launch_rows<64, 8, RES, TU, TY>(x, upd, g, b, res_out, y, rows, eps, affine, rv, mm, s);
+    case 128: return launch_rows<128, 16, RES, TU, TY>(x, upd, g, b, res_out, y, rows, eps, affine, rv, mm, s);
+    case 256: return launch_rows<256, 32, RES, TU, TY>(x, upd, g, b, res_out, y, rows, eps, affine, rv, mm, s);
+    case 512: return launch_rows<512, 64, RES, TU, TY>(x, upd, g, b, res_out, y, rows, eps, affine, rv, mm, s);
+    case 1024: return launch_rows<1024, 64, RES, TU, TY>(x, upd, g, b, res_out, y, rows, eps, affine, rv, mm, s);
+    case 2048: return launch_rows<2048, 64, RES, TU, TY>(x, upd, g, b, res_out, y, rows, eps, affine, rv, mm, s);
     default:
       hipLaunchKernelGGL((ln_generic_kernel<RES, TU, TY>), dim3((unsigned)rows), dim3(256), 0, s,
                          x, static_cast<const TU*>(upd), g, b, res_out, static_cast<TY*>(y),
-                         cols, eps, affine);
+                         cols, eps, affine, rv, mm);
       return hipGetLastError();
   }
 }
@@ -229,31 +258,44 @@ extern "C" int xb_layernorm(const float* x, const float* gamma, const float* bet
   return (int)e;
 }
 
-extern "C" int xb_residual_layernorm(const float* residual, const void* update,
-                                     int update_dtype, const float* gamma,
-                                     const float* beta, float* residual_out, void* y,
-                                     int y_dtype, int64_t rows, int32_t cols, float eps,
-                                     int apply_affine, void* stream) {
+extern "C" int xb_residual_layernorm_masked(const float* residual, const void* update,
+                                            int update_dtype, const float* gamma,
+                                            const float* beta, float* residual_out, void* y,
+                                            int y_dtype, int64_t rows, int32_t cols, float eps,
+                                            int apply_affine, const uint8_t* row_valid,
+                                            int mask_mode, void* stream) {
   if (rows < 0 || cols <= 0 || rows > 0x7fffffffLL) return XB_ERR_BAD_SIZE;
   if (y_dtype != XB_F32 && y_dtype != XB_F16) return XB_ERR_BAD_DTYPE;
   if (update_dtype != XB_F32 && update_dtype != XB_F16) return XB_ERR_BAD_DTYPE;
+  if (mask_mode & ~(XB_MASK_UPDATE | XB_MASK_SUM | XB_MASK_OUTPUT)) return XB_ERR_BAD_EPILOGUE;
   if (rows == 0) return XB_OK;
   if (!residual || !update || !y || (apply_affine && (!gamma || !beta))) return XB_ERR_NULL_POINTER;
+  if (mask_mode != 0 && !row_valid) return XB_ERR_NULL_POINTER;
   if (vector_width(cols) &&
       (!aligned16(residual) || !aligned16(update) || !aligned16(y) ||
        (residual_out && !aligned16(residual_out)) ||
        (apply_affine && (!aligned16(gamma) || !aligned16(beta)))))
     return XB_ERR_MISALIGNED;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const uint8_t* rv = mask_mode != 0 ? row_valid : nullptr;
   hipError_t e;
   if (update_dtype == XB_F16) {
     e = y_dtype == XB_F16
-        ? dispatch_width<true, half_t, half_t>(residual, update, gamma, beta, residual_out, y, rows, cols, eps, apply_affine, s)
-        : dispatch_width<true, half_t, float>(residual, update, gamma, beta, residual_out, y, rows, cols, eps, apply_affine, s);
+        ? dispatch_width<true, half_t, half_t>(residual, update, gamma, beta, residual_out, y, rows, cols, eps, apply_affine, s, rv, mask_mode)
+        : dispatch_width<true, half_t, float>(residual, update, gamma, beta, residual_out, y, rows, cols, eps, apply_affine, s, rv, mask_mode);
   } else {
     e = y_dtype == XB_F16
-        ? dispatch_width<true, float, half_t>(residual, update, gamma, beta, residual_out, y, rows, cols, eps, apply_affine, s)
-        : dispatch_width<true, float, float>(residual, update, gamma, beta, residual_out, y, rows, cols, eps, apply_affine, s);
+        ? dispatch_width<true, float, half_t>(residual, update, gamma, beta, residual_out, y, rows, cols, eps, apply_affine, s, rv, mask_mode)
+        : dispatch_width<true, float, float>(residual, update, gamma, beta, residual_out, y, rows, cols, eps, apply_affine, s, rv, mask_mode);
   }
   return (int)e;
+}
+
+extern "C" int xb_residual_layernorm(const float* residual, const void* update,
+                                     int update_dtype, const float* gamma,
+                                     const float* beta, float* residual_out, void* y,
+                                     int y_dtype, int64_t rows, int32_t cols, float eps,
+                                     int apply_affine, void* stream) {
+  return xb_residual_layernorm_masked(residual, update, update_dtype, gamma, beta, residual_out, y, y_dtype,
+                                      rows, cols, eps, apply_affine, nullptr, 0, stream);
 }

@@ -130,12 +130,20 @@ def fused_residual_layer_norm(
     apply_affine: bool = True,
     residual_out: Optional[torch.Tensor] = None,
     norm_out: Optional[torch.Tensor] = None,
+    row_valid: Optional[torch.Tensor] = None,
+    mask_mode: int = 0,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
     """Return (residual + update in FP32, LayerNorm of it in `norm_dtype`) (FN:173-215).
 
     With store_residual=False the sum is not written and the input `residual`
     object is returned, as in the reference.  `residual_out` / `norm_out` let
     a caller supply destinations (residual_out may be `residual` itself).
+
+    `row_valid` (bool or uint8, one entry per row) with `mask_mode` (a mask of
+    XB_MASK_UPDATE / XB_MASK_SUM / XB_MASK_OUTPUT) applies the baseline's
+    padding rules to the rows whose entry is false: drop the update, zero the
+    sum, zero the normalised output (torch_transformer_benchmark.py:263-264,
+    :290-291, :314-315).
     """
     _require_device(residual, "fused_residual_layer_norm")
     if residual.shape != update.shape:
@@ -157,15 +165,42 @@ def fused_residual_layer_norm(
     rows = residual.numel() // n_cols
     upd_code, norm_code = _dtype_code(update.dtype, "update"), _dtype_code(norm_out.dtype, "norm")
     name = f"residual_layernorm_{n_cols}{'' if store_residual else '_final'}"
-    check(
-        _launch(name, lambda: lib().xb_residual_layernorm(
-            residual.data_ptr(), update.data_ptr(), upd_code, _ptr(weight), _ptr(bias),
-            _ptr(residual_out), norm_out.data_ptr(), norm_code, rows, n_cols, float(eps),
-            int(bool(apply_affine)), stream_handle(residual.device),
-        )),
-        "xb_residual_layernorm",
-    )
+    if row_valid is None:
+        if mask_mode:
+            raise ValueError("mask_mode needs row_valid")
+        check(
+            _launch(name, lambda: lib().xb_residual_layernorm(
+                residual.data_ptr(), update.data_ptr(), upd_code, _ptr(weight), _ptr(bias),
+                _ptr(residual_out), norm_out.data_ptr(), norm_code, rows, n_cols, float(eps),
+                int(bool(apply_affine)), stream_handle(residual.device),
+            )),
+            "xb_residual_layernorm",
+        )
+    else:
+        valid = _byte_mask(row_valid, rows, residual.device, "row_valid")
+        check(
+            _launch(name + "_masked", lambda: lib().xb_residual_layernorm_masked(
+                residual.data_ptr(), update.data_ptr(), upd_code, _ptr(weight), _ptr(bias),
+                _ptr(residual_out), norm_out.data_ptr(), norm_code, rows, n_cols, float(eps),
+                int(bool(apply_affine)), valid.data_ptr(), int(mask_mode),
+                stream_handle(residual.device),
+            )),
+            "xb_residual_layernorm_masked",
+        )
     return (residual_out if store_residual else residual), norm_out
+
+
+def _byte_mask(mask: torch.Tensor, count: int, device: torch.device, what: str) -> torch.Tensor:
+    """`mask` as a contiguous uint8 tensor of `count` entries on `device`."""
+    if mask.numel() != count:
+        raise ValueError(f"{what} must have {count} entries, got {mask.numel()}")
+    if mask.device != device:
+        raise ValueError(f"{what} must be on {device}")
+    if mask.dtype not in (torch.bool, torch.uint8):
+        raise ValueError(f"{what} must be bool or uint8")
+    if mask.dtype == torch.bool:
+        mask = mask.view(torch.uint8) if mask.is_contiguous() else mask.contiguous().view(torch.uint8)
+    return mask.contiguous()
 
 
 def linear(
@@ -229,7 +264,26 @@ def causal_attention(
     (torch_transformer_benchmark.py:742-745).  `scale` defaults to
     head_dim ** -0.5, SDPA's default and the baseline's (TTB:215).
     """
-    _require_device(qkv, "causal_attention")
+    return attention(qkv, num_heads, key_valid=None, causal=True, scale=scale, out=out)
+
+
+def attention(
+    qkv: torch.Tensor,
+    num_heads: int,
+    key_valid: Optional[torch.Tensor] = None,
+    causal: bool = True,
+    scale: Optional[float] = None,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Attention over a packed [B, S, 3*D] FP16 projection with optional key padding.
+
+    key_valid ([B, S] bool/uint8, None = all valid) excludes the keys whose
+    entry is false, the baseline's key padding mask (torch_transformer_benchmark.py:
+    250-253); causal=False drops the causal mask.  A query that sees no key
+    gets a zero row (the baseline's softmax would give NaN there, which its
+    block then overwrites by zeroing the padded rows, TTB:263-264).
+    """
+    _require_device(qkv, "attention")
     if qkv.ndim != 3 or qkv.shape[-1] % (3 * num_heads) != 0:
         raise ValueError("qkv must be [B, S, 3 * num_heads * head_dim]")
     if qkv.dtype != torch.float16 or not qkv.is_contiguous():
@@ -241,12 +295,14 @@ def causal_attention(
         scale = head_dim ** -0.5
     if out is None:
         out = torch.empty((batch, seq_len, d_model), device=qkv.device, dtype=torch.float16)
+    valid = None if key_valid is None else _byte_mask(key_valid, batch * seq_len, qkv.device, "key_valid")
+    name = f"attention_hd{head_dim}{'' if causal else '_full'}{'' if valid is None else '_masked'}"
     check(
-        _launch(f"attention_hd{head_dim}", lambda: lib().xb_attention_causal(
-            qkv.data_ptr(), out.data_ptr(), batch, seq_len, num_heads, head_dim, float(scale),
-            stream_handle(qkv.device),
+        _launch(name, lambda: lib().xb_attention(
+            qkv.data_ptr(), out.data_ptr(), _ptr(valid), batch, seq_len, num_heads, head_dim,
+            float(scale), int(bool(causal)), stream_handle(qkv.device),
         )),
-        "xb_attention_causal",
+        "xb_attention",
     )
     return out
 

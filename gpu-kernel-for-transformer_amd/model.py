@@ -25,6 +25,16 @@ from libxblock.so:
 The residual stream is FP32; GEMM operands are FP16 with FP32 accumulation,
 the storage scheme of the reference's mixed-precision path.  There is no CPU
 or PyTorch-op fallback: inputs that the HIP path cannot serve raise.
+
+A padded `valid_token_mask` is handled as the reference's optimized path does
+(torch_transformer_benchmark.py:497-513): padded tokens are masked as keys in
+every layer's attention and their rows are zeroed only in the final
+LayerNorm's output.  Valid rows therefore equal the baseline's, which also
+zeroes padded rows after each attention and block (TTB:263-264, :290-291) --
+padded rows reach valid ones only as keys, and those are masked.  Unlike the
+reference (TTB:503-508) there is no sequence-length limit: the key mask is a
+[B, S] byte vector read by the attention kernel, not a dense [S, S] mask.
+`config.causal = False` runs the same kernels without the causal mask.
 """
 
 from __future__ import annotations
@@ -34,7 +44,7 @@ from typing import Dict, Optional, Tuple
 import torch
 import torch.nn as nn
 
-from . import kernels
+from . import _capi, kernels
 from .config import ShapeExecutionPlan, TransformerConfig, resolve_shape_execution_plan
 
 _LOG2E = 1.4426950408889634
@@ -253,16 +263,23 @@ class UserOptimizedTransformer(nn.Module):
             )
         if self._mixed_precision_dtype != torch.float16:
             raise NotImplementedError("the gfx950 path implements float16 compute only")
-        if not self.config.causal:
-            raise NotImplementedError("the gfx950 path implements causal attention only")
         if x.ndim != 3 or x.shape[-1] != self.config.d_model:
             raise ValueError(f"expected input [B, S, {self.config.d_model}], got {tuple(x.shape)}")
         if x.dtype != torch.float32:
             raise ValueError("the gfx950 path expects a float32 residual stream input")
         if self.training:
             raise RuntimeError("UserOptimizedTransformer is inference-only; call eval()")
-        if not self._all_tokens_valid(valid_token_mask, x.shape[1]):
-            raise NotImplementedError("padding masks are not implemented by the gfx950 path")
+        token_valid = None
+        if valid_token_mask is not None:
+            if tuple(valid_token_mask.shape) != tuple(x.shape[:2]):
+                raise ValueError(
+                    f"valid_token_mask must be [B, S] = {tuple(x.shape[:2])}, got {tuple(valid_token_mask.shape)}")
+            if valid_token_mask.device != x.device:
+                raise ValueError("valid_token_mask must be on the input's device")
+            if valid_token_mask.dtype not in (torch.bool, torch.uint8):
+                raise ValueError("valid_token_mask must be bool or uint8")
+            if not self._all_tokens_valid(valid_token_mask, x.shape[1]):
+                token_valid = (valid_token_mask != 0).to(torch.uint8).contiguous()
         x = x.contiguous()
         chunk = self._large_batch_chunk_size
         with torch.no_grad():
@@ -270,14 +287,20 @@ class UserOptimizedTransformer(nn.Module):
                 output = torch.empty_like(x)
                 for start in range(0, x.shape[0], chunk):
                     end = min(start + chunk, x.shape[0])
-                    self._forward_hip(x[start:end], out=output[start:end])
+                    self._forward_hip(x[start:end], out=output[start:end],
+                                      token_valid=None if token_valid is None else token_valid[start:end])
                 return output
-            return self._forward_hip(x)
+            return self._forward_hip(x, token_valid=token_valid)
 
-    def _forward_hip(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """The fused kernel sequence of TTB:1092-1148 for one all-valid causal batch."""
+    def _forward_hip(self, x: torch.Tensor, out: Optional[torch.Tensor] = None,
+                     token_valid: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """The fused kernel sequence of TTB:1092-1148 for one batch.
+
+        token_valid: None (every token valid) or a contiguous [B, S] uint8 mask
+        with at least one zero.
+        """
         cfg = self.config
-        if self._uses_fused_stack(x):
+        if token_valid is None and cfg.causal and self._uses_fused_stack(x):
             wpack, ppack = self._fused_stack_parameters()
             return kernels.fused_forward_d128(x, wpack, ppack, cfg.num_heads, cfg.ffn_dim, len(self.layers), out=out)
         batch, seq_len, d_model = x.shape
@@ -295,7 +318,8 @@ class UserOptimizedTransformer(nn.Module):
         for index, layer in enumerate(self.layers):
             w = self._layer_weights(index)
             qkv = kernels.linear(norm, w.qkv_w, w.qkv_b)
-            context = kernels.causal_attention(qkv, cfg.num_heads, layer.attention.scale)
+            context = kernels.attention(qkv, cfg.num_heads, key_valid=token_valid, causal=cfg.causal,
+                                        scale=layer.attention.scale)
             update = kernels.linear(context, w.out_w, w.out_b)
             residual_in, norm2 = kernels.fused_residual_layer_norm(
                 residual_in, update, layer.norm2.weight, layer.norm2.bias, layer.norm2.eps, f16,
@@ -310,6 +334,8 @@ class UserOptimizedTransformer(nn.Module):
                 torch.float32 if last else f16, store_residual=not last,
                 apply_affine=self._layer_norm_uses_affine(following),
                 residual_out=residual, norm_out=out if last else None,
+                row_valid=token_valid if last else None,
+                mask_mode=_capi.XB_MASK_OUTPUT if last and token_valid is not None else 0,
             )
         return norm
 

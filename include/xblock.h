@@ -39,6 +39,11 @@ extern "C" {
 #define XB_EPI_BIAS 0       /* y = acc + bias                                  */
 #define XB_EPI_BIAS_GELU 1  /* y = gelu_erf(acc + bias) (exact erf, not tanh)  */
 
+/* Row masks of xb_residual_layernorm_masked (bits; rows whose valid byte is 0). */
+#define XB_MASK_UPDATE 1    /* the update is dropped: s = residual             */
+#define XB_MASK_SUM 2       /* s = 0 (stored residual and LayerNorm input)    */
+#define XB_MASK_OUTPUT 4    /* y = 0                                           */
+
 int xb_abi_version(void);
 const char* xb_strerror(int code);
 
@@ -68,6 +73,22 @@ int xb_residual_layernorm(const float* residual, const void* update,
                           int apply_affine, void* stream);
 
 /*
+ * xb_residual_layernorm with the reference's padding semantics: for rows whose
+ * row_valid byte is 0, mask_mode selects (by selection, not multiplication, so
+ * NaN in a dropped update does not leak) XB_MASK_UPDATE (attention output
+ * zeroed before the residual add, torch_transformer_benchmark.py:263-264),
+ * XB_MASK_SUM (block output zeroed, :290-291) and XB_MASK_OUTPUT (final
+ * LayerNorm output zeroed, :314-315).  row_valid may be NULL only with
+ * mask_mode 0.
+ */
+int xb_residual_layernorm_masked(const float* residual, const void* update,
+                                 int update_dtype, const float* gamma,
+                                 const float* beta, float* residual_out, void* y,
+                                 int y_dtype, int64_t rows, int32_t cols, float eps,
+                                 int apply_affine, const uint8_t* row_valid,
+                                 int mask_mode, void* stream);
+
+/*
  * c[M, N] = epilogue(a[M, K] . w[N, K]^T + bias[N]) with FP16 operands, FP32
  * MFMA accumulation and an FP16 store.  w is nn.Linear's own [out, in] layout;
  * bias is FP32 (may be NULL for no bias).  K and N must be multiples of 8.
@@ -90,6 +111,18 @@ int xb_linear(const void* a, const void* w, const float* bias, void* c,
 int xb_attention_causal(const void* qkv, void* out, int32_t batch,
                         int64_t seq_len, int32_t heads, int32_t head_dim,
                         float scale, void* stream);
+
+/*
+ * xb_attention_causal generalised: causal = 0 drops the causal mask, and
+ * key_valid ([batch, seq_len] bytes, NULL = all valid) masks keys whose byte
+ * is 0 -- the baseline's key padding mask (torch_transformer_benchmark.py:
+ * 250-253; the reference's optimized path builds the same mask densely in
+ * _prepare_attention_args, :464-522).  A query that sees no key at all writes
+ * zeros.
+ */
+int xb_attention(const void* qkv, void* out, const uint8_t* key_valid,
+                 int32_t batch, int64_t seq_len, int32_t heads,
+                 int32_t head_dim, float scale, int32_t causal, void* stream);
 
 /* Fragment orders of xb_pack_linear_fragments. */
 #define XB_PACK_PERMUTED 0  /* k = 32*ks + 4*(l/16) + (m & 3) + 16*(m >> 2) */

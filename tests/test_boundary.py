@@ -122,6 +122,13 @@ def test_argument_errors_need_no_gpu(capi):
     assert lib.xb_residual_layernorm(16, 16, 1, None, None, None, 16, 1, 0, 128, 1e-5, 0, None) == 0
     assert lib.xb_attention_causal(16, 16, 1, 8, 2, 24, 0.1, None) == -4  # head_dim 24
     assert lib.xb_attention_causal(16, 16, 0, 8, 2, 8, 0.1, None) == 0
+    assert lib.xb_attention(16, 16, None, 1, 8, 2, 24, 0.1, 0, None) == -4   # head_dim 24
+    assert lib.xb_attention(None, None, None, 1, 8, 2, 64, 0.1, 1, None) == -1
+    assert lib.xb_attention(16, 16, None, 0, 8, 2, 64, 0.1, 0, None) == 0    # empty: no launch
+    # mask_mode outside UPDATE|SUM|OUTPUT, and a mask mode without row_valid
+    assert lib.xb_residual_layernorm_masked(16, 16, 1, None, None, None, 16, 1, 4, 128, 1e-5, 0, 16, 8, None) == -6
+    assert lib.xb_residual_layernorm_masked(16, 16, 1, None, None, None, 16, 1, 4, 128, 1e-5, 0, None, 2, None) == -1
+    assert lib.xb_residual_layernorm_masked(16, 16, 1, None, None, None, 16, 1, 0, 128, 1e-5, 0, None, 7, None) == 0
     for code in (0, -1, -2, -3, -4, -5, -6):
         assert lib.xb_strerror(code)
     with pytest.raises(RuntimeError, match="xb_linear failed with code -4"):

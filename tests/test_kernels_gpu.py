@@ -117,15 +117,20 @@ def test_linear_errors(pkg, cuda):
 
 
 # ----------------------------------------------------------------------------- attention
-def _attention_reference(qkv: torch.Tensor, heads: int) -> torch.Tensor:
+def _attention_reference(qkv: torch.Tensor, heads: int, key_valid=None, causal: bool = True) -> torch.Tensor:
+    """FP32 softmax attention; a query with no visible key gets a zero row."""
     b, s, width = qkv.shape
     d = width // 3
     hd = d // heads
     t = qkv.float().view(b, s, 3, heads, hd).permute(2, 0, 3, 1, 4)
     q, k, v = t[0], t[1], t[2]
     scores = (q @ k.transpose(-2, -1)) * hd**-0.5
-    scores = scores.masked_fill(torch.ones(s, s, dtype=torch.bool).triu(1), float("-inf"))
-    return (torch.softmax(scores, -1) @ v).transpose(1, 2).reshape(b, s, d)
+    if causal:
+        scores = scores.masked_fill(torch.ones(s, s, dtype=torch.bool).triu(1), float("-inf"))
+    if key_valid is not None:
+        scores = scores.masked_fill(~key_valid[:, None, None, :], float("-inf"))
+    probs = torch.nan_to_num(torch.softmax(scores, -1), nan=0.0)
+    return (probs @ v).transpose(1, 2).reshape(b, s, d)
 
 
 @pytest.mark.parametrize("hd", [8, 16, 32, 64, 128, 256])
@@ -154,3 +159,95 @@ def test_causal_attention_first_token_is_value(pkg, cuda):
     out = pkg.causal_attention(qkv.to(cuda), 4).cpu()
     v0 = qkv[:, 0, 2 * 128:].float()
     torch.testing.assert_close(out[:, 0].float(), v0, atol=1e-3, rtol=1e-3)
+
+
+def _padding_mask(b: int, s: int, kind: str, seed: int) -> torch.Tensor:
+    gen = _gen(seed)
+    pos = torch.arange(s)[None, :]
+    lengths = torch.randint(1, s + 1, (b,), generator=gen)
+    if kind == "right":
+        return pos < lengths[:, None]
+    if kind == "left":
+        return pos >= (s - lengths)[:, None]
+    mask = torch.rand(b, s, generator=gen) > 0.3
+    if kind == "random_with_empty" and b > 1:
+        mask[1] = False  # a sequence with no valid key at all
+    return mask
+
+
+@pytest.mark.parametrize("hd", [8, 32, 64, 128, 256])
+@pytest.mark.parametrize("b,s,h", [(3, 1, 2), (3, 77, 2), (2, 300, 2), (2, 1100, 1)])
+@pytest.mark.parametrize("kind", ["right", "left", "random_with_empty"])
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_key_padding(pkg, cuda, hd, b, s, h, kind, causal):
+    qkv = torch.randn(b, s, 3 * h * hd, generator=_gen(hd * 31 + s)).half()
+    mask = _padding_mask(b, s, kind, seed=s + hd)
+    ref = _attention_reference(qkv, h, key_valid=mask, causal=causal)
+    out = pkg.attention(qkv.to(cuda), h, key_valid=mask.to(cuda), causal=causal)
+    assert out.shape == (b, s, h * hd)
+    # FP16 probabilities and FP16 output rounding; fully masked queries are exactly zero.
+    torch.testing.assert_close(out.cpu().float(), ref, atol=2e-3, rtol=1e-2)
+
+
+@pytest.mark.parametrize("hd", [16, 64, 128])
+@pytest.mark.parametrize("s", [1, 100, 1500])
+def test_attention_non_causal(pkg, cuda, hd, s):
+    h = 2
+    qkv = torch.randn(2, s, 3 * h * hd, generator=_gen(hd + 7 * s)).half()
+    ref = _attention_reference(qkv, h, causal=False)
+    out = pkg.attention(qkv.to(cuda), h, causal=False)
+    torch.testing.assert_close(out.cpu().float(), ref, atol=2e-3, rtol=1e-2)
+
+
+def test_attention_all_valid_mask_equals_unmasked(pkg, cuda):
+    qkv = torch.randn(2, 257, 3 * 2 * 64, generator=_gen(5)).half().to(cuda)
+    ones = torch.ones(2, 257, dtype=torch.bool, device=cuda)
+    a = pkg.causal_attention(qkv, 2)
+    m = pkg.attention(qkv, 2, key_valid=ones, causal=True)
+    assert torch.equal(a, m)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_large_negative_first_scores(pkg, cuda, causal):
+    """First key tile scores far below zero (2^-185 probabilities before the shift).
+
+    The running offset must jump onto them without rescaling the still-empty
+    accumulators by exp2(185) (= inf, and 0 * inf = NaN).
+    """
+    b, s, h, hd = 1, 192, 1, 64
+    q = torch.full((s, hd), 4.0)
+    k = torch.full((s, hd), 0.05)
+    k[:64] = -4.0                      # q.k * scale * log2(e) = -184.7 for keys 0..63
+    v = torch.randn(s, hd, generator=_gen(11))
+    qkv = torch.cat((q, k, v), 1).reshape(b, s, 3 * hd).half()
+    ref = _attention_reference(qkv, h, causal=causal)
+    out = pkg.attention(qkv.to(cuda), h, causal=causal).cpu().float()
+    assert torch.isfinite(out).all()
+    torch.testing.assert_close(out, ref, atol=2e-3, rtol=1e-2)
+
+
+@pytest.mark.parametrize("cols", [128, 1024, 96])
+@pytest.mark.parametrize("mode", [1, 2, 4, 3, 6, 7])
+def test_residual_layer_norm_row_masks(pkg, cuda, cols, mode):
+    """XB_MASK_UPDATE (1) / XB_MASK_SUM (2) / XB_MASK_OUTPUT (4) on the rows whose flag is 0."""
+    rows = 301
+    r = torch.randn(rows, cols, generator=_gen(13)) * 1.5
+    u = (torch.randn(rows, cols, generator=_gen(14)) * 0.7).half()
+    valid = torch.rand(rows, generator=_gen(15)) > 0.4
+    u[~valid] = float("nan")           # a masked update must not leak (selection, not multiply)
+    g = torch.randn(cols, generator=_gen(16)) * 0.3 + 1.0
+    b = torch.randn(cols, generator=_gen(17)) * 0.1
+    inv = ~valid[:, None]
+    s = r + u.float()
+    if mode & 1:
+        s = torch.where(inv, r, s)
+    if mode & 2:
+        s = torch.where(inv, torch.zeros_like(s), s)
+    ref = F.layer_norm(s, (cols,), g, b, 1e-5)
+    if mode & 4:
+        ref = torch.where(inv, torch.zeros_like(ref), ref)
+    res, norm = pkg.fused_residual_layer_norm(
+        r.to(cuda), u.to(cuda), g.to(cuda), b.to(cuda), 1e-5, F32, row_valid=valid.to(cuda), mask_mode=mode)
+    # Without UPDATE/SUM the masked rows keep the NaN sum, exactly as the reference would.
+    torch.testing.assert_close(res.cpu(), s, atol=0, rtol=0, equal_nan=True)
+    torch.testing.assert_close(norm.cpu(), ref, atol=2e-5, rtol=2e-5, equal_nan=True)

@@ -207,10 +207,92 @@ def test_graph_replay_matches_eager(pkg, cuda):
             del scratch
 
 
-def test_no_padding_support_raises(pkg, cuda):
+def _padded_parity(pkg, cuda, config, x, mask, label):
+    baseline, optimized = _models(pkg, config, cuda)
+    with torch.inference_mode():
+        ref = baseline(x, mask)
+        out = optimized(x.to(cuda), mask.to(cuda)).cpu()
+    # Padded rows are exactly zero in both (TTB:314-315); valid rows meet the rule.
+    assert torch.equal(out[~mask], torch.zeros_like(out[~mask])), f"{label}: padded rows not zero"
+    _check(ref, out, label)
+
+
+@pytest.mark.parametrize(
+    "geom",
+    [
+        (8, 128, 512, 8, 2048, 6, False),  # the reference's default CLI model (TTB:1567-1573)
+        (8, 128, 512, 8, 2048, 6, True),
+        (64, 128, 128, 4, 128, 4, True),   # official shape 1 geometry, padded
+        (3, 77, 256, 4, 512, 2, False),
+        (2, 300, 1024, 4, 1024, 1, True),  # head_dim 256
+    ],
+)
+def test_padding_ratio_parity(pkg, cuda, geom):
+    """The reference's "fixed padding-mask" scenario: padding_ratio 0.25 (VT:61-64)."""
+    config = pkg.TransformerConfig(*geom)
+    for trial in range(2):
+        x, mask = generate_random_case(config, torch.device("cpu"), torch.float32, seed=1234 + trial,
+                                       padding_ratio=0.25)
+        assert not mask.all()
+        _padded_parity(pkg, cuda, config, x, mask, f"padded {geom} trial {trial}")
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_left_padding_and_empty_sequence(pkg, cuda, causal):
+    """Left padding (padded queries with no visible key under the causal mask)
+    and a sequence with no valid token at all (the baseline's softmax is NaN
+    there; its masking zeroes the rows)."""
+    config = pkg.TransformerConfig(4, 70, 128, 2, 256, 2, causal)
+    x = torch.randn(4, 70, 128, generator=torch.Generator().manual_seed(8))
+    mask = torch.ones(4, 70, dtype=torch.bool)
+    mask[0, :13] = False
+    mask[1, :] = False
+    mask[2, 40:] = False
+    mask[3, ::3] = False
+    _padded_parity(pkg, cuda, config, x, mask, f"left/empty causal={causal}")
+
+
+def test_padded_causal_beyond_4096(pkg, cuda):
+    """The reference refuses padded causal inputs above S=4096 (TTB:499-504);
+    the key-mask kernel has no such limit."""
+    config = pkg.TransformerConfig(1, 5000, 128, 2, 128, 1, True)
+    x, mask = generate_random_case(config, torch.device("cpu"), torch.float32, seed=21, padding_ratio=0.3)
+    mask[0, 4500:] = False
+    _padded_parity(pkg, cuda, config, x, mask, "padded causal S=5000")
+
+
+@pytest.mark.parametrize("geom", [(8, 128, 512, 8, 2048, 6), (2, 129, 128, 16, 128, 2), (2, 1100, 256, 4, 256, 1)])
+def test_non_causal_parity(pkg, cuda, geom):
+    """The reference's default CUDA scenario is non-causal (VT:58, TTB:1567-1573)."""
+    config = pkg.TransformerConfig(*geom, False)
+    baseline, optimized = _models(pkg, config, cuda)
+    x, mask = generate_random_case(config, torch.device("cpu"), torch.float32, seed=1234)
+    with torch.inference_mode():
+        ref = baseline(x, mask)
+        out = optimized(x.to(cuda), mask.to(cuda)).cpu()
+    _check(ref, out, f"non-causal {geom}")
+
+
+def test_padded_batch_chunking_matches_unchunked(pkg, cuda):
+    config = pkg.TransformerConfig(40, 32, 128, 4, 128, 2, True)
+    _, optimized = _models(pkg, config, cuda)
+    x, mask = generate_random_case(config, torch.device("cpu"), torch.float32, seed=4, padding_ratio=0.5)
+    xg, mg = x.to(cuda), mask.to(cuda)
+    with torch.inference_mode():
+        whole = optimized(xg, mg)
+        optimized._large_batch_chunk_size = 16
+        chunked = optimized(xg, mg)
+        optimized._large_batch_chunk_size = 0
+    assert torch.equal(whole, chunked)
+
+
+def test_mask_argument_errors(pkg, cuda):
     config = pkg.TransformerConfig(2, 8, 64, 4, 64, 1, True)
     _, optimized = _models(pkg, config, cuda)
-    mask = torch.ones(2, 8, dtype=torch.bool, device=cuda)
-    mask[1, 5:] = False
-    with pytest.raises(NotImplementedError):
-        optimized(torch.randn(2, 8, 64, device=cuda), mask)
+    x = torch.randn(2, 8, 64, device=cuda)
+    with pytest.raises(ValueError):
+        optimized(x, torch.ones(2, 9, dtype=torch.bool, device=cuda))
+    with pytest.raises(ValueError):
+        optimized(x, torch.ones(2, 8, dtype=torch.bool))
+    with pytest.raises(ValueError):
+        optimized(x, torch.ones(2, 8, dtype=torch.float32, device=cuda))

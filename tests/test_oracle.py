@@ -106,6 +106,60 @@ def test_brute_force_rejects_planted_mistakes(mistake, monkeypatch):
         np.testing.assert_allclose(bad, good, rtol=1e-4, atol=1e-4)
 
 
+def _compacted_reference(model, x, mask):
+    """Run each sequence's valid tokens alone, in order, and scatter them back.
+
+    Without positional encodings a padded token enters the baseline only as a
+    masked key, so a padded forward must equal the forward over the valid
+    tokens compacted into a shorter sequence (causal order is kept), with the
+    padded rows zero.
+    """
+    out = torch.zeros_like(x)
+    for b in range(x.shape[0]):
+        idx = torch.nonzero(mask[b]).flatten()
+        if idx.numel() == 0:
+            continue
+        model.config = Cfg(1, idx.numel(), x.shape[2], model.config.num_heads, model.config.ffn_dim,
+                           model.config.num_layers, model.config.causal)
+        with torch.no_grad():
+            out[b, idx] = model(x[b : b + 1, idx].contiguous())[0]
+    return out
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_padding_equals_compaction(causal):
+    """Pins the restated padding semantics (TTB:250-253, :263-264, :290-291, :314-315)."""
+    cfg = Cfg(4, 12, 32, 4, 48, 2, causal)
+    model = _model(cfg)
+    x = torch.randn(4, 12, 32, generator=torch.Generator().manual_seed(17))
+    mask = torch.ones(4, 12, dtype=torch.bool)
+    mask[0, 9:] = False            # right padding
+    mask[1, :5] = False            # left padding (causal: padded queries see no key)
+    mask[2, ::2] = False           # holes
+    mask[3, :] = False             # nothing valid
+    with torch.no_grad():
+        padded = model(x, mask)
+    assert torch.isfinite(padded).all()
+    expected = _compacted_reference(model, x, mask)
+    model.config = cfg
+    torch.testing.assert_close(padded, expected, atol=1e-5, rtol=1e-5)
+
+    # Planted mistake: zeroing padded outputs without masking them as keys.
+    original = BaselineSelfAttention.forward
+
+    def keys_unmasked(self, xx, valid_token_mask=None, causal=False):
+        out = original(self, xx, None, causal)
+        return out if valid_token_mask is None else out.masked_fill(~valid_token_mask[..., None], 0)
+
+    BaselineSelfAttention.forward = keys_unmasked
+    try:
+        with torch.no_grad():
+            bad = model(x, mask)
+    finally:
+        BaselineSelfAttention.forward = original
+    assert not torch.allclose(bad, expected, atol=1e-3, rtol=1e-3)
+
+
 def test_causal_prefix_invariance():
     """out[:, :p] depends only on x[:, :p] (the basis of cfg5's prefix check)."""
     cfg = Cfg(2, 24, 32, 4, 32, 2)
