@@ -36,6 +36,7 @@ sys.path.insert(0, str(REPO))
 HBM_BYTES_PER_S = 8.0e12          # MI355X HBM3E peak
 FP16_MFMA_FLOPS = 2.5166e15       # MI355X dense FP16 MFMA peak (256 CU x 2.4 GHz x 4096)
 CONFIG_NAMES = {1: "cfg1", 6: "cfg2", 8: "cfg3", 11: "cfg4", 14: "cfg5"}
+CPU_SAMPLE_ROWS = {1: 64, 6: 256, 8: 16, 11: 64, 14: 1}
 
 
 def parse_args():
@@ -43,7 +44,8 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--workload", type=int, default=6, choices=sorted(CONFIG_NAMES), help="official shape id of the headline line")
+    p.add_argument("--workload", type=int, default=6, choices=range(1, 15), metavar="SHAPE_ID",
+                   help="official shape id (1-14) of the headline line; default 6 = BASELINE config 2")
     p.add_argument("--no-per-config", action="store_true", help="skip the other four configs")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="bound on the CPU baseline's timed work")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -51,7 +53,30 @@ def parse_args():
     p.add_argument("--copy-calibration", action="store_true",
                    help="with --profile-only: also run a plain 1 GiB elementwise copy (HBM counter calibration)")
     p.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 FETCH_SIZE/WRITE_SIZE runs")
-    return p.parse_args()
+    p.add_argument("--rounds", type=int, default=1, help="headline: median ms over this many timed rounds of --steps")
+    p.add_argument("--batch", type=int, default=0,
+                   help="run the headline with this batch instead of the shape's (the line then says so)")
+    p.add_argument("--accuracy-trials", type=int, default=1,
+                   help="accuracy samples: the timed input, then fresh inputs seeded 1234+t (TTB:1307-1372)")
+    p.add_argument("--strict-accuracy", action="store_true", help="exit with status 2 when an accuracy check fails")
+    args = p.parse_args()
+    if args.steps <= 0 or args.warmup < 0 or args.rounds <= 0 or args.accuracy_trials <= 0 or args.batch < 0:
+        p.error("steps, rounds and accuracy trials must be positive; warmup and batch non-negative")
+    return args
+
+
+def case_name(shape_id: int) -> str:
+    return CONFIG_NAMES.get(shape_id, f"shape{shape_id}")
+
+
+def sample_rows(shape_id: int, config) -> int:
+    """Sequences in the bounded CPU-oracle sample of a workload."""
+    if shape_id in CPU_SAMPLE_ROWS:
+        return CPU_SAMPLE_ROWS[shape_id]
+    if config.seq_len > 8192:
+        return 1
+    budget = 8192 if config.d_model <= 256 else 2048  # tokens per oracle call
+    return max(1, min(config.batch_size, budget // config.seq_len))
 
 
 def kernel_costs(name: str, config, rows: int):
@@ -90,12 +115,12 @@ def log(*a):
 
 
 # Kernel symbol substring of each LaunchRecorder name (for counter CSVs).
-KERNEL_SYMBOLS = (("fused_forward_d128", "fused_stack_kernel"), ("attention", "attn_causal_kernel"),
+KERNEL_SYMBOLS = (("fused_forward_d128", "fused_stack_kernel"), ("attention", "attn_kernel"),
                   ("gemm_", "gemm_"), ("residual_layernorm", "ln_"), ("layernorm", "ln_"))
 CALIBRATION_BYTES = 1 << 30
 
 
-def measure_traffic(workload: int, dominant: str):
+def measure_traffic(workload: int, dominant: str, batch: int = 0):
     """HBM bytes per launch of `dominant` from two rocprofv3 --pmc runs of this script.
 
     Each run (FETCH_SIZE, then WRITE_SIZE) replays the headline workload with
@@ -120,7 +145,7 @@ def measure_traffic(workload: int, dominant: str):
         out_dir = tempfile.mkdtemp(prefix=f"xb_{counter.lower()}_", dir="/tmp")
         cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", out_dir, "-o", "run", "--",
                sys.executable, str(REPO / "bench.py"), "--profile-only", "--copy-calibration",
-               "--workload", str(workload), "--steps", "2", "--warmup", "1"]
+               "--workload", str(workload), "--steps", "2", "--warmup", "1", "--batch", str(batch)]
         try:
             proc = subprocess.run(cmd, cwd="/tmp", capture_output=True, text=True, timeout=240)
         except subprocess.TimeoutExpired:
@@ -192,6 +217,22 @@ def main() -> int:
         wall = time.perf_counter() - t0
         return start.elapsed_time(end) / steps, wall
 
+    def extra_trials(baseline, model, config, rows, trials):
+        """Accuracy of fresh inputs seeded 1234+t, t = 1..trials-1, on `rows` sequences."""
+        from oracle.accuracy import compare_outputs
+
+        results = []
+        for t in range(1, trials):
+            g = torch.Generator(device=device).manual_seed(1234 + t)
+            xt = torch.randn(rows, config.seq_len, config.d_model, generator=g, device=device)
+            with torch.inference_mode():
+                out_t = model(xt)
+                if config.seq_len > 8192:  # long context: causal prefix only
+                    xt, out_t = xt[:, :4096], out_t[:, :4096]
+                ref_t = baseline(xt.float().cpu().contiguous())
+            results.append(compare_outputs(ref_t, out_t.cpu()))
+        return results
+
     def cpu_leg(baseline, config, gpu_out, x_gpu, budget_s, rows_per_call):
         """Oracle on the host cores over a bounded slice; returns rate and accuracy."""
         from oracle.accuracy import compare_outputs
@@ -222,15 +263,21 @@ def main() -> int:
     results = {}
     order = [args.workload] + ([] if (args.no_per_config or args.profile_only) else [i for i in CONFIG_NAMES if i != args.workload])
     headline = None
+    accuracy_failed = False
     for shape_id in order:
         config = pkg.OFFICIAL_BENCHMARK_SHAPES[shape_id]
-        name = CONFIG_NAMES[shape_id]
+        name = case_name(shape_id)
+        is_head = shape_id == args.workload
+        if is_head and args.batch and args.batch != config.batch_size:
+            import dataclasses
+
+            config = dataclasses.replace(config, batch_size=args.batch)
+            name = f"{name}-b{args.batch}"
         log(f"[bench] {name} (official shape {shape_id}): {config}")
         baseline, model = build(config)
         x = make_input(config, 1234 + 100000)
         tokens = config.batch_size * config.seq_len
         big = config.seq_len > 8192
-        is_head = shape_id == args.workload
         if big:
             steps, warmup = (max(1, min(args.steps, 3)), 1) if is_head else (2, 1)
         else:
@@ -246,8 +293,11 @@ def main() -> int:
                 graphed = graphs.FixedInputCUDAGraph(model, x, None)
                 run = lambda: graphed(x)  # noqa: E731  (clone included, as the reference's replay)
                 mode = "hipGraph replay"
-            if is_head or big:
+            if big or (is_head and args.rounds == 1):
                 ms, wall = time_steps(run, steps, warmup)
+            elif is_head:
+                rounds = [time_steps(run, steps, warmup if r == 0 else 0) for r in range(args.rounds)]
+                ms, wall = statistics.median(r[0] for r in rounds), sum(r[1] for r in rounds)
             else:
                 rounds = [time_steps(run, steps, warmup if r == 0 else 0) for r in range(3)]
                 ms, wall = statistics.median(r[0] for r in rounds), sum(r[1] for r in rounds)
@@ -261,7 +311,15 @@ def main() -> int:
         t_bound = max(fl / FP16_MFMA_FLOPS, by / HBM_BYTES_PER_S)
         entry_["bound"] = "mfma" if fl / FP16_MFMA_FLOPS > by / HBM_BYTES_PER_S else "hbm"
         entry_["roofline_frac"] = t_bound / (ms / 1e3)
-        log(f"[bench] {name}: {ms:.3f} ms/step, {entry_['tokens_per_s']:.4g} tokens/s ({mode}), roofline frac {entry_['roofline_frac']:.3f}")
+        # Against the fully fused lower bound: read x, write y, weights once.
+        by_min = 8.0 * tokens * config.d_model + 2.0 * config.num_layers * (
+            4 * config.d_model ** 2 + 2 * config.d_model * config.ffn_dim)
+        t_min = max(fl / FP16_MFMA_FLOPS, by_min / HBM_BYTES_PER_S)
+        entry_["bound_min"] = "mfma" if fl / FP16_MFMA_FLOPS > by_min / HBM_BYTES_PER_S else "hbm"
+        entry_["roofline_frac_min"] = t_min / (ms / 1e3)
+        log(f"[bench] {name}: {ms:.3f} ms/step, {entry_['tokens_per_s']:.4g} tokens/s ({mode}), roofline frac "
+            f"{entry_['roofline_frac']:.3f} of the kernel pipeline's {entry_['bound']} bound, "
+            f"{entry_['roofline_frac_min']:.3f} of the fused lower bound ({entry_['bound_min']})")
 
         if is_head:
             headline = dict(entry_, config=config, wall=wall)
@@ -289,13 +347,19 @@ def main() -> int:
             if args.no_cpu_baseline and not is_head:
                 pass
             else:
-                rows = {1: 64, 6: 256, 8: 16, 11: 64, 14: 1}[shape_id]
+                rows = sample_rows(shape_id, config)
                 budget = args.cpu_seconds if is_head else min(args.cpu_seconds, 5.0)
                 if args.no_cpu_baseline:
                     budget = 0.0
                 cpu, acc = cpu_leg(baseline, config, out, x, budget, rows)
-                entry_["accuracy"] = {"failed": acc.failed_elements, "total": acc.total_elements,
-                                      "max_abs": acc.max_abs_error, "passed": acc.passed}
+                checks = [acc] + (extra_trials(baseline, model, config, rows, args.accuracy_trials) if is_head else [])
+                entry_["accuracy"] = {"failed": sum(c.failed_elements for c in checks),
+                                      "total": sum(c.total_elements for c in checks),
+                                      "max_abs": max(c.max_abs_error for c in checks),
+                                      "passed": all(c.passed for c in checks), "trials": len(checks)}
+                accuracy_failed |= not entry_["accuracy"]["passed"]
+                if len(checks) > 1:
+                    log(f"[bench] {name}: {len(checks)} accuracy trials: " + "; ".join(c.summary() for c in checks))
                 entry_["cpu_baseline_tokens_per_s"] = cpu["value"]
                 log(f"[bench] {name}: accuracy {acc.summary()}; CPU FP32 oracle {cpu['value']:.4g} tokens/s on {cpu['cores']} threads ({cpu['sample']})")
                 if is_head:
@@ -323,6 +387,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": headline["steps"],
         "warmup": args.warmup,
+        "rounds": args.rounds,
         "ms_per_step": headline["ms"],
         "higher_is_better": True,
         "scaling": "weak",
@@ -330,11 +395,15 @@ def main() -> int:
         "dtype": "fp16",
         "data": "synthetic (x ~ N(0,1) seeded; nn.Linear default init, seed 1234)",
         "config": {
-            "workload": f"{CONFIG_NAMES[args.workload]}: official shape {args.workload}, causal pre-norm block forward",
+            "workload": f"{case_name(args.workload)}: official shape {args.workload}, causal pre-norm block forward"
+                        + (f" at batch {cfg.batch_size}" if args.batch else ""),
             "batch": cfg.batch_size, "seq_len": cfg.seq_len, "d_model": cfg.d_model, "heads": cfg.num_heads,
             "ffn_dim": cfg.ffn_dim, "layers": cfg.num_layers, "mode": headline["mode"],
         },
         "roofline_frac_forward": headline["roofline_frac"],
+        "bound_forward": headline["bound"],
+        "roofline_frac_forward_min": headline["roofline_frac_min"],
+        "bound_forward_min": headline["bound_min"],
     }
     if "dominant" in headline:
         k = headline["kernels"][headline["dominant"]]
@@ -347,7 +416,7 @@ def main() -> int:
                                "frac": round(v["frac"], 4), "bound": v["bound"]} for n, v in headline["kernels"].items()}
     if "dominant" in headline and not args.no_traffic:
         log(f"[bench] HBM traffic of {headline['dominant']}: two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE)")
-        traffic, detail = measure_traffic(args.workload, headline["dominant"])
+        traffic, detail = measure_traffic(args.workload, headline["dominant"], args.batch)
         line["roofline"]["traffic"] = traffic
         line["roofline"]["traffic_detail"] = detail
         if traffic is not None:
@@ -360,6 +429,9 @@ def main() -> int:
     if len(results) > 1:
         line["per_config"] = {n: {k: (round(v, 6) if isinstance(v, float) else v) for k, v in r.items()} for n, r in results.items()}
     print(json.dumps(line), flush=True)
+    if args.strict_accuracy and accuracy_failed:
+        log("[bench] accuracy check FAILED")
+        return 2
     return 0
 
 
