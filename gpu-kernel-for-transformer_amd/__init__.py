@@ -19,7 +19,16 @@ from .config import (
     TransformerConfig,
     resolve_shape_execution_plan,
 )
-from .kernels import attention, causal_attention, ffn_gelu, fused_residual_layer_norm, layer_norm, linear
+from .kernels import (
+    attention,
+    attention_kv_cache,
+    causal_attention,
+    ffn_gelu,
+    fused_residual_layer_norm,
+    kv_cache_append,
+    layer_norm,
+    linear,
+)
 from .model import (
     SelfAttentionParameters,
     TransformerBlockParameters,
@@ -40,11 +49,13 @@ __all__ = [
     "XBLOCK_AVAILABLE",
     "XBLOCK_LOAD_ERROR",
     "attention",
+    "attention_kv_cache",
     "causal_attention",
     "ffn_gelu",
     "forward_bytes",
     "forward_flops",
     "fused_residual_layer_norm",
+    "kv_cache_append",
     "layer_norm",
     "linear",
     "resolve_shape_execution_plan",

@@ -45,6 +45,9 @@ EXPORTED_SYMBOLS = (
     "xb_linear",
     "xb_attention_causal",
     "xb_attention",
+    "xb_kv_cache_append",
+    "xb_attention_kv_cache_workspace_bytes",
+    "xb_attention_kv_cache",
     "xb_pack_linear_fragments",
     "xb_fused_forward_d128",
 )
@@ -69,6 +72,12 @@ _SIGNATURES = {
     "xb_linear": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, ctypes.c_int, _vp]),
     "xb_attention_causal": (ctypes.c_int, [_vp, _vp, _i32, _i64, _i32, _i32, _f32, _vp]),
     "xb_attention": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i64, _i32, _i32, _f32, _i32, _vp]),
+    "xb_kv_cache_append": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i64, _i32, _i32, _i64, _i64, _vp]),
+    "xb_attention_kv_cache_workspace_bytes": (_i64, [_i32, _i64, _i32, _i32, _i64]),
+    "xb_attention_kv_cache": (
+        ctypes.c_int,
+        [_vp, _vp, _vp, _vp, _i32, _i64, _i32, _i32, _i64, _i64, _f32, _vp, _i64, _vp],
+    ),
     "xb_pack_linear_fragments": (ctypes.c_int, [_vp, _vp, _i32, _i32, _i32, _f32, _vp]),
     "xb_fused_forward_d128": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp]),
 }

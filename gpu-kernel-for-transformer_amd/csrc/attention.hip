@@ -34,18 +34,22 @@
 // exceeds it by more than 8 (probabilities then stay <= 2^8, exact enough in
 // FP16); the decision is wave-uniform.  Only tiles that straddle the diagonal
 // pay for the mask.
+#include <algorithm>
+#include <type_traits>
+
 #include "common.h"
 #include "../../include/xblock.h"
 
 namespace xb {
 
-template <int HD, int NQ>
+template <int HD, int NQ, int NW = 4>
 struct AttnCfg {
+  static constexpr int NT = 64 * NW;                  // threads per block
   static constexpr int BKEYS = HD >= 256 ? 32 : 64;   // keys per LDS tile
   static constexpr int HDP = HD < 32 ? 32 : HD;       // K columns incl. zero pad (S^T reduction)
   static constexpr int HDV = HD < 16 ? 16 : HD;       // V columns incl. zero pad (O^T rows)
   static constexpr int QPW = 16 * NQ;                 // queries per wave
-  static constexpr int BQ = 4 * QPW;                  // queries per block
+  static constexpr int BQ = NW * QPW;                 // queries per block
   static constexpr int LDK = HDP + 8;                 // K tile row stride (halves)
   // V tile row stride (halves): a multiple of 16 halves with an odd quotient
   // (row stride an odd multiple of 32 bytes), which spreads the 32 rows x 8
@@ -53,7 +57,27 @@ struct AttnCfg {
   static constexpr int LDV = (HDV / 16) % 2 ? HDV : HDV + 16;
   static constexpr int KSTEPS = HDP / 32, KB = BKEYS / 16, HB = HDV / 16, KT = BKEYS / 32;
   static constexpr int CPK = HD / 8;                  // 16-byte chunks per key row
-  static constexpr int CH = (BKEYS * CPK + 255) / 256;  // chunks per thread per tile
+  static constexpr int CH = (BKEYS * CPK + NT - 1) / NT;  // chunks per thread per tile
+};
+
+// Where the operands live.  Query, key and value rows of token t of batch b,
+// head h start at q + b*q_bstride + h*HD + t*q_rstride (likewise k, v with
+// k_bstride, k_hstride, k_rstride; the context at out + b*o_bstride + h*HD +
+// t*o_rstride).  The packed [B, S, 3, H, hd] projection and the [B, H, cap, hd]
+// KV cache are both such strided views.  Query i has position q_offset + i;
+// under the causal mask it sees keys j <= q_offset + i.
+struct AttnArgs {
+  const half_t* q;
+  const half_t* k;
+  const half_t* v;
+  half_t* out;
+  const uint8_t* key_valid;  // [B, S_k] bytes (KEYMASK only)
+  float* ws_o;               // split partials: [B*H][splits][BQ][HD] (SPLIT only)
+  float2* ws_ml;             // split partials: [B*H][splits][BQ] (offset, row sum)
+  int64_t q_bstride, k_bstride, k_hstride, o_bstride;
+  int q_rstride, k_rstride, o_rstride;
+  int H, S_q, S_k, q_offset, q_tiles, n_splits, split_keys;
+  float scale_log2;
 };
 
 typedef short short4_t __attribute__((ext_vector_type(4)));
@@ -64,33 +88,43 @@ __device__ __forceinline__ half4_t lds_read_tr16(const half_t* p) {
   return __builtin_bit_cast(half4_t, v);
 }
 
-// CAUSAL: apply the top-left causal mask.  KEYMASK: key_valid ([B, S] bytes,
-// nonzero = the key may be attended to -- the reference's valid_token_mask,
-// TTB:250-253) is staged per tile and masks keys; a query may then see no key
-// in a tile, or at all.  Without KEYMASK every query sees key 0 in the first
+// CAUSAL: apply the causal mask (with the query offset).  KEYMASK: key_valid
+// ([B, S_k] bytes, nonzero = the key may be attended to -- the reference's
+// valid_token_mask, TTB:250-253) is staged per tile and masks keys; a query
+// may then see no key in a tile, or at all.  SPLIT: the block covers all
+// S_q <= BQ queries of one (batch, head) but only keys [split*split_keys,
+// +split_keys), and writes its unnormalised partial (o, offset, row sum) for
+// attn_split_combine; that is the decode path, which needs the whole GPU on
+// the key axis.  Without KEYMASK or SPLIT every query sees key 0 in the first
 // tile, which keeps the offset bookkeeping to a tile-index test.
-template <int HD, int NQ, bool CAUSAL, bool KEYMASK>
-__global__ __launch_bounds__(256, 2) void attn_kernel(
-    const half_t* __restrict__ qkv, half_t* __restrict__ out, const uint8_t* __restrict__ key_valid,
-    int H, int S, int q_tiles, float scale_log2) {
-  using C = AttnCfg<HD, NQ>;
-  constexpr int BKEYS = C::BKEYS, HDP = C::HDP, HDV = C::HDV, QPW = C::QPW, BQ = C::BQ;
+template <int HD, int NQ, int NW, bool CAUSAL, bool KEYMASK, bool SPLIT>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void attn_kernel(const AttnArgs a) {
+  using C = AttnCfg<HD, NQ, NW>;
+  constexpr int NT = C::NT, BKEYS = C::BKEYS, HDP = C::HDP, HDV = C::HDV, QPW = C::QPW, BQ = C::BQ;
   constexpr int LDK = C::LDK, LDV = C::LDV, KSTEPS = C::KSTEPS, KB = C::KB, HB = C::HB;
   constexpr int KT = C::KT, CPK = C::CPK, CH = C::CH;
+  constexpr bool TRACK = KEYMASK || SPLIT;  // a query may see no key in its first tile
+  // One-wave split blocks keep a single LDS tile (the next one waits in
+  // registers), so more of them fit on a CU.
+  constexpr int NBUF = SPLIT ? 1 : 2;
+  static_assert(NT >= BKEYS, "one thread per key stages the validity bytes");
 
-  __shared__ __attribute__((aligned(16))) half_t k_lds[2][BKEYS * LDK];
-  __shared__ __attribute__((aligned(16))) half_t v_lds[2][BKEYS * LDV];
-  __shared__ __attribute__((aligned(16))) uint8_t kv_lds[2][BKEYS];  // key validity of the tile
+  __shared__ __attribute__((aligned(16))) half_t k_lds[NBUF][BKEYS * LDK];
+  __shared__ __attribute__((aligned(16))) half_t v_lds[NBUF][BKEYS * LDV];
+  __shared__ __attribute__((aligned(16))) uint8_t kv_lds[NBUF][BKEYS];  // key validity of the tile
 
   // Heaviest query tiles (most keys under the causal mask) are issued first.
-  const int bh = blockIdx.x / q_tiles;
-  const int qt = CAUSAL ? q_tiles - 1 - (blockIdx.x % q_tiles) : blockIdx.x % q_tiles;
-  const int b = bh / H, h = bh % H;
-  const int D = H * HD;
-  const int64_t row_stride = 3 * (int64_t)D;  // halves between consecutive tokens
-  const half_t* base = qkv + (int64_t)b * S * row_stride + (int64_t)h * HD;
-  const half_t* kbase = base + D;
-  const half_t* vbase = base + 2 * D;
+  const int per_bh = SPLIT ? a.n_splits : a.q_tiles;
+  const int bh = blockIdx.x / per_bh;
+  const int sub = blockIdx.x % per_bh;
+  const int qt = SPLIT ? 0 : (CAUSAL ? a.q_tiles - 1 - sub : sub);
+  const int b = bh / a.H, h = bh % a.H;
+  const int S_q = a.S_q, S_k = a.S_k, q_offset = a.q_offset;
+  const half_t* base = a.q + (int64_t)b * a.q_bstride + (int64_t)h * HD;
+  const int64_t q_rstride = a.q_rstride, k_rstride = a.k_rstride;
+  const half_t* kbase = a.k + (int64_t)b * a.k_bstride + (int64_t)h * a.k_hstride;
+  const half_t* vbase = a.v + (int64_t)b * a.k_bstride + (int64_t)h * a.k_hstride;
+  const float scale_log2 = a.scale_log2;
 
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int g = lane / 16, r16 = lane % 16;
@@ -99,13 +133,13 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(
 
   // Zero the padding columns of both buffers once; tile stores never touch them.
   if constexpr (HDP > HD) {
-    for (int i = tid; i < 2 * BKEYS * (HDP - HD); i += 256) {
+    for (int i = tid; i < NBUF * BKEYS * (HDP - HD); i += NT) {
       const int buf = i / (BKEYS * (HDP - HD)), j = i % (BKEYS * (HDP - HD));
       k_lds[buf][(j / (HDP - HD)) * LDK + HD + j % (HDP - HD)] = (half_t)0.f;
     }
   }
   if constexpr (HDV > HD) {
-    for (int i = tid; i < 2 * BKEYS * (HDV - HD); i += 256) {
+    for (int i = tid; i < NBUF * BKEYS * (HDV - HD); i += NT) {
       const int buf = i / (BKEYS * (HDV - HD)), j = i % (BKEYS * (HDV - HD));
       v_lds[buf][(j / (HDV - HD)) * LDV + HD + j % (HDV - HD)] = (half_t)0.f;
     }
@@ -122,8 +156,8 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(
     for (int ks = 0; ks < KSTEPS; ++ks) {
       const int d = 32 * ks + 8 * g;
       half8_t v = zero8;
-      if (q < S && d < HD) {
-        v = *reinterpret_cast<const half8_t*>(base + q * row_stride + d);
+      if (q < S_q && d < HD) {
+        v = *reinterpret_cast<const half8_t*>(base + q * q_rstride + d);
 #pragma unroll
         for (int m = 0; m < 8; ++m) v[m] = (half_t)((float)v[m] * scale_log2);
       }
@@ -134,7 +168,7 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(
   // m_run: the base-2 exponent offset of query (l % 16) of block qb.  The score
   // MFMAs start from -m_run, so a tile's scores arrive already shifted; the
   // first tile with a visible key for a query moves m_run onto that tile's
-  // exact maximum (m_set records that it happened; without KEYMASK that is
+  // exact maximum (m_set records that it happened; without TRACK that is
   // always tile 0).
   float4_t o[HB][NQ], lacc[NQ];
   float m_run[NQ];
@@ -150,24 +184,24 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(
   const half8_t ones8 = {1, 1, 1, 1, 1, 1, 1, 1};
 
   // Key validity travels with the tile (0 past S as well).
-  const uint8_t* kvb = KEYMASK ? key_valid + (int64_t)b * S : nullptr;
+  const uint8_t* kvb = KEYMASK ? a.key_valid + (int64_t)b * S_k : nullptr;
   uint8_t kvreg = 0;
   half8_t kreg[CH], vreg[CH];
   auto gload = [&](int k0) {
     if (KEYMASK && tid < BKEYS) {
       const int key = k0 + tid;
-      kvreg = key < S ? kvb[key] : (uint8_t)0;
+      kvreg = key < S_k ? kvb[key] : (uint8_t)0;
     }
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
-      const int id = tid + 256 * j;
+      const int id = tid + NT * j;
       kreg[j] = zero8;
       vreg[j] = zero8;
       if (id < BKEYS * CPK) {
         const int key = k0 + id / CPK, c = (id % CPK) * 8;
-        if (key < S) {
-          kreg[j] = *reinterpret_cast<const half8_t*>(kbase + key * row_stride + c);
-          vreg[j] = *reinterpret_cast<const half8_t*>(vbase + key * row_stride + c);
+        if (key < S_k) {
+          kreg[j] = *reinterpret_cast<const half8_t*>(kbase + key * k_rstride + c);
+          vreg[j] = *reinterpret_cast<const half8_t*>(vbase + key * k_rstride + c);
         }
       }
     }
@@ -176,7 +210,7 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(
     if (KEYMASK && tid < BKEYS) kv_lds[buf][tid] = kvreg;
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
-      const int id = tid + 256 * j;
+      const int id = tid + NT * j;
       if (id < BKEYS * CPK) {
         const int r = id / CPK, c = (id % CPK) * 8;
         *reinterpret_cast<half8_t*>(&k_lds[buf][r * LDK + c]) = kreg[j];
@@ -185,19 +219,23 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(
     }
   };
 
-  const int key_end = CAUSAL ? min(S, q0 + BQ) : S;
-  const int n_tiles = (key_end + BKEYS - 1) / BKEYS;
-  gload(0);
-  sstore(0);
+  const int k_begin = SPLIT ? sub * a.split_keys : 0;
+  int key_end = CAUSAL ? min(S_k, q_offset + q0 + BQ) : S_k;
+  if constexpr (SPLIT) key_end = min(key_end, k_begin + a.split_keys);
+  const int n_tiles = key_end > k_begin ? (key_end - k_begin + BKEYS - 1) / BKEYS : 0;
+  if (n_tiles > 0) {
+    gload(k_begin);
+    sstore(0);
+  }
   __syncthreads();
   for (int t = 0; t < n_tiles; ++t) {
-    const int cur = t & 1;
-    const int k0 = t * BKEYS;
+    const int cur = NBUF == 1 ? 0 : t & 1;
+    const int k0 = k_begin + t * BKEYS;
     if (t + 1 < n_tiles) gload(k0 + BKEYS);
 
     // Wave-uniform skip: every key of this tile lies above this wave's diagonal.
-    if (!CAUSAL || k0 <= qw0 + QPW - 1) {
-      const bool diag = CAUSAL && (k0 + BKEYS - 1 > qw0);
+    if (!CAUSAL || k0 <= q_offset + qw0 + QPW - 1) {
+      const bool diag = CAUSAL && (k0 + BKEYS - 1 > q_offset + qw0);
       // Non-causal tiles that run past S mask those keys (causal ones already do).
       const half_t* kt_lds = k_lds[cur];
       const half_t* vt_lds = v_lds[cur];
@@ -227,7 +265,7 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(
           for (int qb = 0; qb < NQ; ++qb)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-              if (k0 + 16 * jb + 4 * g + i > qw0 + 16 * qb + r16) s[jb][qb][i] = -INFINITY;
+              if (k0 + 16 * jb + 4 * g + i > q_offset + qw0 + 16 * qb + r16) s[jb][qb][i] = -INFINITY;
       }
       if constexpr (KEYMASK) {
 #pragma unroll
@@ -239,12 +277,12 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(
 #pragma unroll
               for (int qb = 0; qb < NQ; ++qb) s[jb][qb][i] = -INFINITY;
         }
-      } else if (!CAUSAL && k0 + BKEYS > S) {
+      } else if (!CAUSAL && k0 + BKEYS > S_k) {
 #pragma unroll
         for (int jb = 0; jb < KB; ++jb)
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            if (k0 + 16 * jb + 4 * g + i >= S)
+            if (k0 + 16 * jb + 4 * g + i >= S_k)
 #pragma unroll
               for (int qb = 0; qb < NQ; ++qb) s[jb][qb][i] = -INFINITY;
       }
@@ -258,7 +296,7 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(
       bool unset = t == 0;
 #pragma unroll
       for (int qb = 0; qb < NQ; ++qb) {
-        if constexpr (KEYMASK) unset |= !m_set[qb];
+        if constexpr (TRACK) unset |= !m_set[qb];
 #pragma unroll
         for (int jb = 0; jb < KB; ++jb)
           lm = fmaxf(lm, fmaxf(fmaxf(s[jb][qb][0], s[jb][qb][1]), fmaxf(s[jb][qb][2], s[jb][qb][3])));
@@ -274,9 +312,9 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(
           // Until a query has seen a key its o and lacc are exactly zero: the
           // offset jumps to the first finite maximum and nothing is rescaled
           // (exp2(-sh) could overflow there).  Afterwards sh >= 0, corr <= 1.
-          const bool was_set = KEYMASK ? m_set[qb] : t != 0;
-          const float sh = was_set ? fmaxf(mx, 0.f) : (KEYMASK && mx == -INFINITY ? 0.f : mx);
-          if constexpr (KEYMASK) m_set[qb] = was_set || mx != -INFINITY;
+          const bool was_set = TRACK ? m_set[qb] : t != 0;
+          const float sh = was_set ? fmaxf(mx, 0.f) : (TRACK && mx == -INFINITY ? 0.f : mx);
+          if constexpr (TRACK) m_set[qb] = was_set || mx != -INFINITY;
           const float corr = was_set ? __builtin_amdgcn_exp2f(-sh) : 1.f;
           m_run[qb] += sh;
 #pragma unroll
@@ -314,19 +352,39 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(
     }
 
     __builtin_amdgcn_s_setprio(0);
-    if (t + 1 < n_tiles) sstore(cur ^ 1);
+    if constexpr (NBUF == 1) __syncthreads();  // the tile is read completely before it is replaced
+    if (t + 1 < n_tiles) sstore(NBUF == 1 ? 0 : cur ^ 1);
     __syncthreads();
+  }
+
+  if constexpr (SPLIT) {
+    // Unnormalised partial of this key range: o, the offset m_run (-inf when
+    // the range showed the query no key) and the row sum.
+    const int64_t slot = (int64_t)bh * a.n_splits + sub;
+#pragma unroll
+    for (int qb = 0; qb < NQ; ++qb) {
+      const int q = qw0 + 16 * qb + r16;
+      if (q >= S_q) continue;
+      float* wo = a.ws_o + (slot * BQ + q) * HD;
+#pragma unroll
+      for (int hb = 0; hb < HB; ++hb) {
+        const int d = 16 * hb + 4 * g;
+        if (d < HD) *reinterpret_cast<float4_t*>(wo + d) = o[hb][qb];
+      }
+      if (g == 0) a.ws_ml[slot * BQ + q] = make_float2(m_set[qb] ? m_run[qb] : -INFINITY, lacc[qb][0]);
+    }
+    return;
   }
 
   // Normalise and store: lane holds O^T[16hb + 4g + i][query r16]; every row of
   // the all-ones block holds that query's probability sum.
-  half_t* obase = out + (int64_t)b * S * D + (int64_t)h * HD;
+  half_t* obase = a.out + (int64_t)b * a.o_bstride + (int64_t)h * HD;
 #pragma unroll
   for (int qb = 0; qb < NQ; ++qb) {
     // A query that saw no key at all (every key masked) writes zeros.
     const float inv = lacc[qb][0] > 0.f ? __builtin_amdgcn_rcpf(lacc[qb][0]) : 0.f;
     const int q = qw0 + 16 * qb + r16;
-    if (q >= S) continue;
+    if (q >= S_q) continue;
 #pragma unroll
     for (int hb = 0; hb < HB; ++hb) {
       const int d = 16 * hb + 4 * g;
@@ -334,47 +392,164 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(
         half4_t r;
 #pragma unroll
         for (int i = 0; i < 4; ++i) r[i] = (half_t)(o[hb][qb][i] * inv);
-        *reinterpret_cast<half4_t*>(obase + (int64_t)q * D + d) = r;
+        *reinterpret_cast<half4_t*>(obase + (int64_t)q * a.o_rstride + d) = r;
       }
     }
   }
 }
 
+// Merges the key-range partials of attn_kernel<..., SPLIT>: per (batch, head,
+// query) M = max_s m_s, out = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s.
+// One thread per 8 context columns.
+template <int HD>
+__global__ __launch_bounds__(256) void attn_split_combine(const AttnArgs a, int BQ, int64_t total) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= total) return;
+  constexpr int C8 = HD / 8;
+  const int c = (int)(idx % C8);
+  const int64_t rest = idx / C8;
+  const int q = (int)(rest % a.S_q);
+  const int64_t bh = rest / a.S_q;
+  const int b = (int)(bh / a.H), h = (int)(bh % a.H);
+  const float2* ml = a.ws_ml + bh * a.n_splits * BQ + q;
+  float m = -INFINITY;
+  for (int s = 0; s < a.n_splits; ++s) m = fmaxf(m, ml[(int64_t)s * BQ].x);
+  float l = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < a.n_splits; ++s) {
+    const float2 p = ml[(int64_t)s * BQ];
+    if (p.x == -INFINITY) continue;
+    const float w = __builtin_amdgcn_exp2f(p.x - m);
+    l = fmaf(w, p.y, l);
+    const float* wo = a.ws_o + ((bh * a.n_splits + s) * BQ + q) * HD + 8 * c;
+    const float4_t lo = *reinterpret_cast<const float4_t*>(wo);
+    const float4_t hi = *reinterpret_cast<const float4_t*>(wo + 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acc[i] = fmaf(w, lo[i], acc[i]);
+      acc[4 + i] = fmaf(w, hi[i], acc[4 + i]);
+    }
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  half8_t r;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = (half_t)(acc[i] * inv);
+  *reinterpret_cast<half8_t*>(a.out + (int64_t)b * a.o_bstride + (int64_t)q * a.o_rstride +
+                              (int64_t)h * HD + 8 * c) = r;
+}
+
 template <int HD, int NQ>
-static hipError_t launch_attn(const half_t* qkv, half_t* out, const uint8_t* kv, int B, int S, int H,
-                              float scale, int causal, hipStream_t s) {
+static hipError_t launch_attn(AttnArgs a, int B, int causal, hipStream_t s) {
   constexpr int BQ = AttnCfg<HD, NQ>::BQ;
-  const int q_tiles = (S + BQ - 1) / BQ;
-  const int64_t blocks = (int64_t)q_tiles * B * H;
+  a.q_tiles = (a.S_q + BQ - 1) / BQ;
+  const int64_t blocks = (int64_t)a.q_tiles * B * a.H;
   if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
-  const float scale_log2 = scale * 1.44269504088896340736f;
-  const dim3 grid((unsigned)blocks);
-  if (kv != nullptr) {
+  const dim3 grid((unsigned)blocks), block(AttnCfg<HD, NQ>::NT);
+  if (a.key_valid != nullptr) {
     if (causal)
-      hipLaunchKernelGGL((attn_kernel<HD, NQ, true, true>), grid, dim3(256), 0, s, qkv, out, kv, H, S, q_tiles, scale_log2);
+      hipLaunchKernelGGL((attn_kernel<HD, NQ, 4, true, true, false>), grid, block, 0, s, a);
     else
-      hipLaunchKernelGGL((attn_kernel<HD, NQ, false, true>), grid, dim3(256), 0, s, qkv, out, kv, H, S, q_tiles, scale_log2);
+      hipLaunchKernelGGL((attn_kernel<HD, NQ, 4, false, true, false>), grid, block, 0, s, a);
   } else {
     if (causal)
-      hipLaunchKernelGGL((attn_kernel<HD, NQ, true, false>), grid, dim3(256), 0, s, qkv, out, kv, H, S, q_tiles, scale_log2);
+      hipLaunchKernelGGL((attn_kernel<HD, NQ, 4, true, false, false>), grid, block, 0, s, a);
     else
-      hipLaunchKernelGGL((attn_kernel<HD, NQ, false, false>), grid, dim3(256), 0, s, qkv, out, kv, H, S, q_tiles, scale_log2);
+      hipLaunchKernelGGL((attn_kernel<HD, NQ, 4, false, false, false>), grid, block, 0, s, a);
   }
   return hipGetLastError();
 }
 
-// Long sequences take 64 queries per wave (each K/V fragment read from LDS
-// then feeds 4 MFMAs); short ones keep 32 so a block does not outgrow S.
+// Long query ranges take 64 queries per wave (each K/V fragment read from LDS
+// then feeds 4 MFMAs); short ones keep 32 so a block does not outgrow S_q.
 template <int HD>
-static hipError_t dispatch_attn(const half_t* qkv, half_t* out, const uint8_t* kv, int B, int S, int H,
-                                float scale, int causal, hipStream_t s) {
+static hipError_t dispatch_attn(const AttnArgs& a, int B, int causal, hipStream_t s) {
   if constexpr (HD >= 256) {
-    return launch_attn<HD, 1>(qkv, out, kv, B, S, H, scale, causal, s);
+    return launch_attn<HD, 1>(a, B, causal, s);
   } else if constexpr (HD >= 128) {
-    return launch_attn<HD, 2>(qkv, out, kv, B, S, H, scale, causal, s);
+    return launch_attn<HD, 2>(a, B, causal, s);
   } else {
-    if (S >= 1024) return launch_attn<HD, 4>(qkv, out, kv, B, S, H, scale, causal, s);
-    return launch_attn<HD, 2>(qkv, out, kv, B, S, H, scale, causal, s);
+    if (a.S_q >= 1024) return launch_attn<HD, 4>(a, B, causal, s);
+    return launch_attn<HD, 2>(a, B, causal, s);
+  }
+}
+
+// Decode (at most kDecodeQueries new tokens per sequence): one-wave blocks,
+// each over a range of whole key tiles, sized so B*H*splits comes to about
+// eight waves per CU when the cache is long enough.
+constexpr int kDecodeQueries = 16;
+constexpr int64_t kDecodeTargetBlocks = 2048;
+
+struct DecodeGeometry {
+  int n_splits, split_keys;
+  int64_t o_bytes, bytes;  // partial o, then (offset, sum) pairs
+};
+
+static DecodeGeometry decode_geometry(int B, int H, int S_k, int HD) {
+  const int bk = HD >= 256 ? 32 : 64;
+  const int tiles = (S_k + bk - 1) / bk;
+  const int64_t bh = (int64_t)B * H;
+  const int64_t want = std::min<int64_t>(tiles, std::max<int64_t>(1, (kDecodeTargetBlocks + bh - 1) / bh));
+  const int tiles_per = (int)((tiles + want - 1) / want);
+  DecodeGeometry g;
+  g.split_keys = tiles_per * bk;
+  g.n_splits = (S_k + g.split_keys - 1) / g.split_keys;
+  const int64_t slots = bh * g.n_splits * kDecodeQueries;
+  g.o_bytes = slots * HD * (int64_t)sizeof(float);
+  g.bytes = g.o_bytes + slots * (int64_t)sizeof(float2);
+  return g;
+}
+
+template <int HD>
+static hipError_t launch_decode(AttnArgs a, int B, const DecodeGeometry& geo, void* workspace, hipStream_t s) {
+  static_assert(AttnCfg<HD, 1, 1>::BQ == kDecodeQueries, "one wave of 16 queries");
+  a.n_splits = geo.n_splits;
+  a.split_keys = geo.split_keys;
+  a.ws_o = static_cast<float*>(workspace);
+  a.ws_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) + geo.o_bytes);
+  const int64_t blocks = (int64_t)B * a.H * geo.n_splits;
+  if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((attn_kernel<HD, 1, 1, true, false, true>), dim3((unsigned)blocks), dim3(64), 0, s, a);
+  const int64_t total = (int64_t)B * a.H * a.S_q * (HD / 8);
+  const int64_t cblocks = (total + 255) / 256;
+  if (cblocks > 0x7fffffffLL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((attn_split_combine<HD>), dim3((unsigned)cblocks), dim3(256), 0, s, a, kDecodeQueries, total);
+  return hipGetLastError();
+}
+
+// Copies the new tokens' keys and values out of the packed projection into
+// the [B, H, capacity, hd] caches at positions start .. start + chunk - 1.
+// One thread per 16 bytes of K (and the same 16 bytes of V).
+__global__ __launch_bounds__(256) void kv_append_kernel(const half_t* __restrict__ qkv, half_t* __restrict__ kc,
+                                                       half_t* __restrict__ vc, int H, int HD, int chunk,
+                                                       int64_t start, int64_t cap, int64_t total) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= total) return;
+  const int c8 = HD / 8;
+  const int c = (int)(idx % c8);
+  int64_t rest = idx / c8;
+  const int h = (int)(rest % H);
+  rest /= H;
+  const int t = (int)(rest % chunk);
+  const int64_t b = rest / chunk;
+  const int64_t D = (int64_t)H * HD;
+  const half_t* src = qkv + (b * chunk + t) * 3 * D + D + (int64_t)h * HD + 8 * c;
+  const int64_t dst = ((b * H + h) * cap + start + t) * HD + 8 * c;
+  *reinterpret_cast<half8_t*>(kc + dst) = *reinterpret_cast<const half8_t*>(src);
+  *reinterpret_cast<half8_t*>(vc + dst) = *reinterpret_cast<const half8_t*>(src + D);
+}
+
+static bool supported_head_dim(int hd) {
+  return hd == 8 || hd == 16 || hd == 32 || hd == 64 || hd == 128 || hd == 256;
+}
+
+template <typename F>
+static hipError_t by_head_dim(int hd, F&& f) {
+  switch (hd) {
+    case 8: return f(std::integral_constant<int, 8>());
+    case 16: return f(std::integral_constant<int, 16>());
+    case 32: return f(std::integral_constant<int, 32>());
+    case 64: return f(std::integral_constant<int, 64>());
+    case 128: return f(std::integral_constant<int, 128>());
+    default: return f(std::integral_constant<int, 256>());
   }
 }
 
@@ -387,30 +562,103 @@ extern "C" int xb_attention(const void* qkv, void* out, const uint8_t* key_valid
                             void* stream) {
   if (batch < 0 || seq_len < 0 || heads <= 0 || head_dim <= 0) return XB_ERR_BAD_SIZE;
   if (seq_len > 0x7fffffffLL / 4) return XB_ERR_BAD_SIZE;
-  if (head_dim != 8 && head_dim != 16 && head_dim != 32 && head_dim != 64 && head_dim != 128 &&
-      head_dim != 256)
-    return XB_ERR_UNSUPPORTED_SHAPE;
+  if (!supported_head_dim(head_dim)) return XB_ERR_UNSUPPORTED_SHAPE;
   if (batch == 0 || seq_len == 0) return XB_OK;  // empty tensors may carry NULL data pointers
   if (!qkv || !out) return XB_ERR_NULL_POINTER;
   if (((uintptr_t)qkv | (uintptr_t)out) & 15u) return XB_ERR_MISALIGNED;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const half_t* q = static_cast<const half_t*>(qkv);
-  half_t* o = static_cast<half_t*>(out);
   const int S = (int)seq_len;
+  const int64_t D = (int64_t)heads * head_dim;
+  AttnArgs a = {};
+  a.q = static_cast<const half_t*>(qkv);
+  a.k = a.q + D;
+  a.v = a.q + 2 * D;
+  a.out = static_cast<half_t*>(out);
+  a.key_valid = key_valid;
+  a.q_bstride = a.k_bstride = (int64_t)S * 3 * D;
+  a.k_hstride = head_dim;
+  a.o_bstride = (int64_t)S * D;
+  a.q_rstride = a.k_rstride = (int)(3 * D);
+  a.o_rstride = (int)D;
+  a.H = heads;
+  a.S_q = a.S_k = S;
+  a.scale_log2 = scale * 1.44269504088896340736f;
+  if (3 * D > 0x7fffffffLL) return XB_ERR_BAD_SIZE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
   const int c = causal ? 1 : 0;
-  hipError_t e;
-  switch (head_dim) {
-    case 8: e = dispatch_attn<8>(q, o, key_valid, batch, S, heads, scale, c, s); break;
-    case 16: e = dispatch_attn<16>(q, o, key_valid, batch, S, heads, scale, c, s); break;
-    case 32: e = dispatch_attn<32>(q, o, key_valid, batch, S, heads, scale, c, s); break;
-    case 64: e = dispatch_attn<64>(q, o, key_valid, batch, S, heads, scale, c, s); break;
-    case 128: e = dispatch_attn<128>(q, o, key_valid, batch, S, heads, scale, c, s); break;
-    default: e = dispatch_attn<256>(q, o, key_valid, batch, S, heads, scale, c, s); break;
-  }
-  return (int)e;
+  return (int)by_head_dim(head_dim, [&](auto hd) { return dispatch_attn<decltype(hd)::value>(a, batch, c, s); });
 }
 
 extern "C" int xb_attention_causal(const void* qkv, void* out, int32_t batch, int64_t seq_len,
                                    int32_t heads, int32_t head_dim, float scale, void* stream) {
   return xb_attention(qkv, out, nullptr, batch, seq_len, heads, head_dim, scale, 1, stream);
+}
+
+static int check_cache_args(int32_t batch, int64_t chunk, int32_t heads, int32_t head_dim, int64_t start,
+                            int64_t capacity) {
+  if (batch < 0 || chunk < 0 || heads <= 0 || head_dim <= 0 || start < 0 || capacity < 0) return XB_ERR_BAD_SIZE;
+  if (capacity > 0x7fffffffLL / 4 || start + chunk > capacity) return XB_ERR_BAD_SIZE;
+  if (3LL * heads * head_dim > 0x7fffffffLL) return XB_ERR_BAD_SIZE;
+  if (!supported_head_dim(head_dim)) return XB_ERR_UNSUPPORTED_SHAPE;
+  return XB_OK;
+}
+
+extern "C" int xb_kv_cache_append(const void* qkv, void* k_cache, void* v_cache, int32_t batch, int64_t chunk,
+                                  int32_t heads, int32_t head_dim, int64_t start, int64_t capacity, void* stream) {
+  const int bad = check_cache_args(batch, chunk, heads, head_dim, start, capacity);
+  if (bad) return bad;
+  if (batch == 0 || chunk == 0) return XB_OK;
+  if (!qkv || !k_cache || !v_cache) return XB_ERR_NULL_POINTER;
+  if (((uintptr_t)qkv | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15u) return XB_ERR_MISALIGNED;
+  const int64_t total = (int64_t)batch * chunk * heads * (head_dim / 8);
+  const int64_t blocks = (total + 255) / 256;
+  if (blocks > 0x7fffffffLL) return XB_ERR_BAD_SIZE;
+  hipLaunchKernelGGL(kv_append_kernel, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const half_t*>(qkv), static_cast<half_t*>(k_cache), static_cast<half_t*>(v_cache),
+                     heads, head_dim, (int)chunk, start, capacity, total);
+  return (int)hipGetLastError();
+}
+
+extern "C" int64_t xb_attention_kv_cache_workspace_bytes(int32_t batch, int64_t chunk, int32_t heads,
+                                                         int32_t head_dim, int64_t start) {
+  const int bad = check_cache_args(batch, chunk, heads, head_dim, start, start + chunk);
+  if (bad) return bad;
+  if (batch == 0 || chunk == 0 || chunk > kDecodeQueries) return 0;
+  return decode_geometry(batch, heads, (int)(start + chunk), head_dim).bytes;
+}
+
+extern "C" int xb_attention_kv_cache(const void* qkv, const void* k_cache, const void* v_cache, void* out,
+                                     int32_t batch, int64_t chunk, int32_t heads, int32_t head_dim, int64_t start,
+                                     int64_t capacity, float scale, void* workspace, int64_t workspace_bytes,
+                                     void* stream) {
+  const int bad = check_cache_args(batch, chunk, heads, head_dim, start, capacity);
+  if (bad) return bad;
+  if (batch == 0 || chunk == 0) return XB_OK;
+  if (!qkv || !k_cache || !v_cache || !out) return XB_ERR_NULL_POINTER;
+  if (((uintptr_t)qkv | (uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)out) & 15u) return XB_ERR_MISALIGNED;
+  const int64_t D = (int64_t)heads * head_dim;
+  AttnArgs a = {};
+  a.q = static_cast<const half_t*>(qkv);
+  a.k = static_cast<const half_t*>(k_cache);
+  a.v = static_cast<const half_t*>(v_cache);
+  a.out = static_cast<half_t*>(out);
+  a.q_bstride = chunk * 3 * D;
+  a.q_rstride = (int)(3 * D);
+  a.k_bstride = heads * capacity * head_dim;
+  a.k_hstride = capacity * head_dim;
+  a.k_rstride = head_dim;
+  a.o_bstride = chunk * D;
+  a.o_rstride = (int)D;
+  a.H = heads;
+  a.S_q = (int)chunk;
+  a.S_k = (int)(start + chunk);
+  a.q_offset = (int)start;
+  a.scale_log2 = scale * 1.44269504088896340736f;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (chunk > kDecodeQueries)
+    return (int)by_head_dim(head_dim, [&](auto hd) { return dispatch_attn<decltype(hd)::value>(a, batch, 1, s); });
+  const DecodeGeometry geo = decode_geometry(batch, heads, a.S_k, head_dim);
+  if (!workspace) return XB_ERR_NULL_POINTER;
+  if (workspace_bytes < geo.bytes) return XB_ERR_WORKSPACE;
+  if ((uintptr_t)workspace & 15u) return XB_ERR_MISALIGNED;
+  return (int)by_head_dim(head_dim, [&](auto hd) { return launch_decode<decltype(hd)::value>(a, batch, geo, workspace, s); });
 }

@@ -88,6 +88,8 @@ def maybe_cuda_graph(model: nn.Module, x: torch.Tensor, valid_token_mask: Option
         return model, False, "graphs require a GPU input"
     if bool(getattr(model, "_uses_internal_cuda_graphs", False)):
         return model, True, str(getattr(model, "graph_status", "internal graph replay"))
+    if bool(getattr(model, "_kv_cache_enabled", False)):
+        return model, False, "stateful KV-cache decoding uses the eager path"
     try:
         with torch.inference_mode():
             eager = model(x, valid_token_mask)

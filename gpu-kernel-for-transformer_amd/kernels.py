@@ -307,6 +307,84 @@ def attention(
     return out
 
 
+def _check_kv_cache(qkv: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, num_heads: int) -> Tuple[int, int, int, int]:
+    if qkv.ndim != 3 or qkv.shape[-1] % (3 * num_heads) != 0:
+        raise ValueError("qkv must be [B, chunk, 3 * num_heads * head_dim]")
+    if qkv.dtype != torch.float16 or not qkv.is_contiguous():
+        raise ValueError("qkv must be contiguous float16")
+    batch, chunk, width = qkv.shape
+    head_dim = width // 3 // num_heads
+    for name, cache in (("k_cache", k_cache), ("v_cache", v_cache)):
+        if cache.ndim != 4 or cache.shape[0] != batch or cache.shape[1] != num_heads or cache.shape[3] != head_dim:
+            raise ValueError(f"{name} must be [B, heads, capacity, head_dim] = [{batch}, {num_heads}, *, {head_dim}]")
+        if cache.dtype != torch.float16 or not cache.is_contiguous() or cache.device != qkv.device:
+            raise ValueError(f"{name} must be contiguous float16 on the projection's device")
+    if k_cache.shape != v_cache.shape:
+        raise ValueError("k_cache and v_cache must have the same shape")
+    return batch, chunk, head_dim, k_cache.shape[2]
+
+
+def kv_cache_append(qkv: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, num_heads: int, start: int) -> None:
+    """Write the chunk's keys and values into the caches at positions start.. (TTB:426-462)."""
+    _require_device(qkv, "kv_cache_append")
+    batch, chunk, head_dim, capacity = _check_kv_cache(qkv, k_cache, v_cache, num_heads)
+    if start < 0 or start + chunk > capacity:
+        raise ValueError(f"KV cache capacity exceeded ({start + chunk} > {capacity})")
+    check(
+        _launch(f"kv_append_hd{head_dim}", lambda: lib().xb_kv_cache_append(
+            qkv.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), batch, chunk, num_heads, head_dim,
+            int(start), capacity, stream_handle(qkv.device))),
+        "xb_kv_cache_append",
+    )
+
+
+def attention_kv_cache(
+    qkv: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    num_heads: int,
+    start: int,
+    scale: Optional[float] = None,
+    out: Optional[torch.Tensor] = None,
+    workspace: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Causal attention of a chunk at positions start.. over the cached keys 0..start+chunk-1.
+
+    Call after kv_cache_append for the same chunk (TTB:747-765).  `workspace`
+    (uint8, at least kv_cache_workspace_bytes) is allocated here when not
+    given; decode chunks of up to 16 tokens need one.
+    """
+    _require_device(qkv, "attention_kv_cache")
+    batch, chunk, head_dim, capacity = _check_kv_cache(qkv, k_cache, v_cache, num_heads)
+    if start < 0 or start + chunk > capacity:
+        raise ValueError(f"KV cache capacity exceeded ({start + chunk} > {capacity})")
+    if scale is None:
+        scale = head_dim ** -0.5
+    d_model = num_heads * head_dim
+    if out is None:
+        out = torch.empty((batch, chunk, d_model), device=qkv.device, dtype=torch.float16)
+    need = kv_cache_workspace_bytes(batch, chunk, num_heads, head_dim, start)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, device=qkv.device, dtype=torch.uint8)
+    ws_ptr = workspace.data_ptr() if need else None
+    ws_bytes = workspace.numel() * workspace.element_size() if need else 0
+    check(
+        _launch(f"attention_kv_hd{head_dim}{'_decode' if need else ''}", lambda: lib().xb_attention_kv_cache(
+            qkv.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(), batch, chunk, num_heads,
+            head_dim, int(start), capacity, float(scale), ws_ptr, ws_bytes, stream_handle(qkv.device))),
+        "xb_attention_kv_cache",
+    )
+    return out
+
+
+def kv_cache_workspace_bytes(batch: int, chunk: int, num_heads: int, head_dim: int, start: int) -> int:
+    """Workspace bytes xb_attention_kv_cache needs (0 for chunks longer than 16 tokens)."""
+    need = lib().xb_attention_kv_cache_workspace_bytes(batch, chunk, num_heads, head_dim, int(start))
+    if need < 0:
+        check(int(need), "xb_attention_kv_cache_workspace_bytes")
+    return int(need)
+
+
 def pack_linear_fragments(weight: torch.Tensor, natural: bool = False, scale: float = 1.0) -> torch.Tensor:
     """FP16 fragment-major copy of `scale * weight` (nn.Linear [n, k]) for the fused kernel.
 

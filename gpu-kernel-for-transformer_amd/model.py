@@ -130,6 +130,7 @@ class UserOptimizedTransformer(nn.Module):
         # enable_mixed_precision(torch.float16) (TTB:1750-1771).
         self._mixed_precision_dtype: Optional[torch.dtype] = torch.float16
         self._kv_cache_enabled = False
+        self._kv_cache: Dict[int, Tuple[torch.Tensor, torch.Tensor]] = {}
         self._kv_cache_length = 0
         self._large_batch_chunk_size = self._shape_execution_plan.batch_chunk_size
         self._fused_stack_enabled = True
@@ -157,13 +158,22 @@ class UserOptimizedTransformer(nn.Module):
         self._fused_stack_enabled = bool(enabled)
 
     def enable_kv_cache(self, enabled: bool = True) -> None:
-        """KV-cached decoding (TTB:408-417) is not part of the HIP path."""
-        if enabled:
-            raise NotImplementedError("KV-cached decoding is not implemented by the gfx950 path")
-        self._kv_cache_enabled = False
+        """Incremental decoding over a per-layer FP16 KV cache, clearing any previous sequence (TTB:408-415).
+
+        Each forward then appends its tokens (positions kv_cache_length ..)
+        to the cache of capacity config.seq_len and attends causally over
+        everything cached so far.
+        """
+        if enabled and not self.config.causal:
+            raise ValueError("KV caching requires a causal Transformer")
+        if enabled and self.training:
+            raise RuntimeError("call eval() before enabling the KV cache")
+        self._kv_cache_enabled = bool(enabled)
         self.reset_kv_cache()
 
     def reset_kv_cache(self) -> None:
+        """Clear cached keys and values before starting a new sequence (TTB:417-420)."""
+        self._kv_cache.clear()
         self._kv_cache_length = 0
 
     @property
@@ -281,6 +291,11 @@ class UserOptimizedTransformer(nn.Module):
             if not self._all_tokens_valid(valid_token_mask, x.shape[1]):
                 token_valid = (valid_token_mask != 0).to(torch.uint8).contiguous()
         x = x.contiguous()
+        if self._kv_cache_enabled:
+            if token_valid is not None:
+                raise ValueError("KV-cached decoding does not support padding")
+            with torch.no_grad():
+                return self._forward_hip_cached(x)
         chunk = self._large_batch_chunk_size
         with torch.no_grad():
             if chunk and x.shape[0] > chunk:
@@ -303,6 +318,55 @@ class UserOptimizedTransformer(nn.Module):
         if token_valid is None and cfg.causal and self._uses_fused_stack(x):
             wpack, ppack = self._fused_stack_parameters()
             return kernels.fused_forward_d128(x, wpack, ppack, cfg.num_heads, cfg.ffn_dim, len(self.layers), out=out)
+
+        def attend(index: int, layer: TransformerBlockParameters, qkv: torch.Tensor) -> torch.Tensor:
+            return kernels.attention(qkv, cfg.num_heads, key_valid=token_valid, causal=cfg.causal,
+                                     scale=layer.attention.scale)
+
+        return self._per_op_forward(x, attend, out=out, token_valid=token_valid)
+
+    def _forward_hip_cached(self, x: torch.Tensor) -> torch.Tensor:
+        """One KV-cached step: append this chunk's keys/values per layer, attend over the cache.
+
+        Caches are [B, H, config.seq_len, hd] FP16 per layer, allocated on the
+        first step (TTB:426-462).  The prompt (position 0) attends within its
+        own projection; later chunks read the cache, decode-sized ones (<= 16
+        tokens) through the split-key kernel.
+        """
+        cfg = self.config
+        batch, chunk, _ = x.shape
+        start = self._kv_cache_length
+        capacity = cfg.seq_len
+        if start + chunk > capacity:
+            raise ValueError(f"KV cache capacity exceeded ({start + chunk} > {capacity})")
+        expected = (batch, cfg.num_heads, capacity, cfg.head_dim)
+        for index in range(len(self.layers)):
+            cached = self._kv_cache.get(index)
+            if cached is None:
+                self._kv_cache[index] = tuple(
+                    torch.empty(expected, device=x.device, dtype=torch.float16) for _ in range(2))
+            elif tuple(cached[0].shape) != expected or cached[0].device != x.device:
+                raise RuntimeError(
+                    "KV cache does not match this input; reset it before changing batch size, device, or dtype")
+        need = kernels.kv_cache_workspace_bytes(batch, chunk, cfg.num_heads, cfg.head_dim, start) if start else 0
+        workspace = torch.empty(need, device=x.device, dtype=torch.uint8) if need else None
+
+        def attend(index: int, layer: TransformerBlockParameters, qkv: torch.Tensor) -> torch.Tensor:
+            k_cache, v_cache = self._kv_cache[index]
+            kernels.kv_cache_append(qkv, k_cache, v_cache, cfg.num_heads, start)
+            if start == 0:
+                return kernels.attention(qkv, cfg.num_heads, causal=True, scale=layer.attention.scale)
+            return kernels.attention_kv_cache(qkv, k_cache, v_cache, cfg.num_heads, start,
+                                              scale=layer.attention.scale, workspace=workspace)
+
+        output = self._per_op_forward(x, attend)
+        self._kv_cache_length = start + chunk
+        return output
+
+    def _per_op_forward(self, x: torch.Tensor, attend, out: Optional[torch.Tensor] = None,
+                        token_valid: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """LN -> per layer (QKV GEMM, attend(index, layer, qkv), out GEMM, residual LN, FFN) -> final LN."""
+        cfg = self.config
         batch, seq_len, d_model = x.shape
         rows = batch * seq_len
         dev = x.device
@@ -318,8 +382,7 @@ class UserOptimizedTransformer(nn.Module):
         for index, layer in enumerate(self.layers):
             w = self._layer_weights(index)
             qkv = kernels.linear(norm, w.qkv_w, w.qkv_b)
-            context = kernels.attention(qkv, cfg.num_heads, key_valid=token_valid, causal=cfg.causal,
-                                        scale=layer.attention.scale)
+            context = attend(index, layer, qkv)
             update = kernels.linear(context, w.out_w, w.out_b)
             residual_in, norm2 = kernels.fused_residual_layer_norm(
                 residual_in, update, layer.norm2.weight, layer.norm2.bias, layer.norm2.eps, f16,

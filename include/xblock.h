@@ -30,6 +30,7 @@ extern "C" {
 #define XB_ERR_UNSUPPORTED_SHAPE (-4)
 #define XB_ERR_MISALIGNED (-5)
 #define XB_ERR_BAD_EPILOGUE (-6)
+#define XB_ERR_WORKSPACE (-7)   /* workspace_bytes below what the call needs */
 
 /* Element types of activations. */
 #define XB_F32 0
@@ -123,6 +124,39 @@ int xb_attention_causal(const void* qkv, void* out, int32_t batch,
 int xb_attention(const void* qkv, void* out, const uint8_t* key_valid,
                  int32_t batch, int64_t seq_len, int32_t heads,
                  int32_t head_dim, float scale, int32_t causal, void* stream);
+
+/*
+ * KV cache for incremental causal decoding (replaces _append_kv_cache and the
+ * cached branch of _fast_attention_impl, torch_transformer_benchmark.py:
+ * 426-462, :747-765).  Per layer the cache is two FP16 tensors k_cache,
+ * v_cache of shape [batch, heads, capacity, head_dim] (the reference's
+ * layout); a forward over `chunk` new tokens whose packed projection is qkv
+ * ([batch, chunk, 3, heads, head_dim]) first appends, then attends:
+ *
+ *   xb_kv_cache_append: k/v_cache[:, :, start:start+chunk] = the chunk's k, v.
+ *   xb_attention_kv_cache: out ([batch, chunk, heads*head_dim] FP16) = causal
+ *     attention of the chunk's queries, at positions start .. start+chunk-1,
+ *     over cached keys 0 .. start+chunk-1 (call it after the append).
+ *
+ * start + chunk <= capacity, else XB_ERR_BAD_SIZE (the reference raises
+ * ValueError, TTB:434-438).  A chunk of at most 16 tokens (decode) splits
+ * the keys over the GPU and needs a caller-provided workspace of
+ * xb_attention_kv_cache_workspace_bytes(...) bytes (16-byte aligned; 0 for
+ * longer chunks, which need none); a smaller one gives XB_ERR_WORKSPACE.
+ */
+int xb_kv_cache_append(const void* qkv, void* k_cache, void* v_cache,
+                       int32_t batch, int64_t chunk, int32_t heads,
+                       int32_t head_dim, int64_t start, int64_t capacity,
+                       void* stream);
+int64_t xb_attention_kv_cache_workspace_bytes(int32_t batch, int64_t chunk,
+                                              int32_t heads, int32_t head_dim,
+                                              int64_t start);
+int xb_attention_kv_cache(const void* qkv, const void* k_cache,
+                          const void* v_cache, void* out, int32_t batch,
+                          int64_t chunk, int32_t heads, int32_t head_dim,
+                          int64_t start, int64_t capacity, float scale,
+                          void* workspace, int64_t workspace_bytes,
+                          void* stream);
 
 /* Fragment orders of xb_pack_linear_fragments. */
 #define XB_PACK_PERMUTED 0  /* k = 32*ks + 4*(l/16) + (m & 3) + 16*(m >> 2) */

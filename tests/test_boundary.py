@@ -78,10 +78,14 @@ def test_toggles(pkg):
     with pytest.raises(ValueError):
         model.enable_mixed_precision(torch.float32)
     model.enable_mixed_precision(torch.float16)
-    with pytest.raises(NotImplementedError):
-        model.enable_kv_cache(True)
+    with pytest.raises(RuntimeError, match="eval"):
+        model.enable_kv_cache(True)           # still in training mode (TTB:412-413)
+    model.eval().enable_kv_cache(True)
+    assert model.kv_cache_length == 0
     model.enable_kv_cache(False)
     assert model.kv_cache_length == 0
+    with pytest.raises(ValueError, match="causal"):
+        pkg.UserOptimizedTransformer(pkg.TransformerConfig(1, 4, 32, 4, 32, 1, False)).eval().enable_kv_cache(True)
     assert model.shape_execution_plan.official_shape_id is None
 
 
@@ -94,7 +98,7 @@ def test_product_never_touches_the_oracle():
 # ----------------------------------------------------------------------------- C-ABI
 def _declared_symbols():
     header = (REPO / "include" / "xblock.h").read_text()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(xb_\w+)\s*\(", header, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(xb_\w+)\s*\(", header, re.M)))
 
 
 def test_library_exports_every_declared_symbol(capi):
@@ -125,11 +129,20 @@ def test_argument_errors_need_no_gpu(capi):
     assert lib.xb_attention(16, 16, None, 1, 8, 2, 24, 0.1, 0, None) == -4   # head_dim 24
     assert lib.xb_attention(None, None, None, 1, 8, 2, 64, 0.1, 1, None) == -1
     assert lib.xb_attention(16, 16, None, 0, 8, 2, 64, 0.1, 0, None) == 0    # empty: no launch
+    # KV cache: capacity, head_dim, workspace sizing without a GPU
+    assert lib.xb_kv_cache_append(16, 16, 16, 1, 5, 2, 64, 10, 12, None) == -2   # 10 + 5 > 12
+    assert lib.xb_kv_cache_append(16, 16, 16, 1, 5, 2, 24, 0, 12, None) == -4
+    assert lib.xb_kv_cache_append(None, None, None, 1, 5, 2, 64, 0, 12, None) == -1
+    assert lib.xb_attention_kv_cache_workspace_bytes(1, 17, 2, 64, 100) == 0     # long chunk: none needed
+    assert lib.xb_attention_kv_cache_workspace_bytes(1, 1, 16, 64, 20000) == 7096320
+    assert lib.xb_attention_kv_cache_workspace_bytes(1, 1, 2, 24, 100) == -4
+    assert lib.xb_attention_kv_cache(16, 16, 16, 16, 1, 1, 2, 64, 100, 101, 0.1, None, 0, None) == -1
+    assert lib.xb_attention_kv_cache(16, 16, 16, 16, 1, 1, 2, 64, 100, 101, 0.1, 16, 64, None) == -7
     # mask_mode outside UPDATE|SUM|OUTPUT, and a mask mode without row_valid
     assert lib.xb_residual_layernorm_masked(16, 16, 1, None, None, None, 16, 1, 4, 128, 1e-5, 0, 16, 8, None) == -6
     assert lib.xb_residual_layernorm_masked(16, 16, 1, None, None, None, 16, 1, 4, 128, 1e-5, 0, None, 2, None) == -1
     assert lib.xb_residual_layernorm_masked(16, 16, 1, None, None, None, 16, 1, 0, 128, 1e-5, 0, None, 7, None) == 0
-    for code in (0, -1, -2, -3, -4, -5, -6):
+    for code in (0, -1, -2, -3, -4, -5, -6, -7):
         assert lib.xb_strerror(code)
     with pytest.raises(RuntimeError, match="xb_linear failed with code -4"):
         capi.check(-4, "xb_linear")

@@ -251,3 +251,78 @@ def test_residual_layer_norm_row_masks(pkg, cuda, cols, mode):
     # Without UPDATE/SUM the masked rows keep the NaN sum, exactly as the reference would.
     torch.testing.assert_close(res.cpu(), s, atol=0, rtol=0, equal_nan=True)
     torch.testing.assert_close(norm.cpu(), ref, atol=2e-5, rtol=2e-5, equal_nan=True)
+
+
+# ----------------------------------------------------------------------------- KV cache
+def _fill_cache(pkg, qkv_full, heads, capacity, pieces, cuda):
+    """Append qkv_full's tokens to fresh caches in the given chunk sizes."""
+    b, length, width = qkv_full.shape
+    hd = width // 3 // heads
+    kc = torch.full((b, heads, capacity, hd), 7.0, dtype=F16, device=cuda)   # sentinel
+    vc = torch.full_like(kc, -7.0)
+    start = 0
+    for n in pieces:
+        pkg.kv_cache_append(qkv_full[:, start:start + n].contiguous().to(cuda), kc, vc, heads, start)
+        start += n
+    assert start == length
+    return kc, vc
+
+
+def test_kv_cache_append_layout(pkg, cuda):
+    b, heads, hd, capacity = 2, 3, 32, 40
+    qkv = torch.randn(b, 23, 3 * heads * hd, generator=_gen(31)).half()
+    kc, vc = _fill_cache(pkg, qkv, heads, capacity, [1, 16, 6], cuda)
+    t = qkv.view(b, 23, 3, heads, hd).permute(2, 0, 3, 1, 4)   # which, b, h, s, hd
+    assert torch.equal(kc[:, :, :23].cpu(), t[1])
+    assert torch.equal(vc[:, :, :23].cpu(), t[2])
+    assert (kc[:, :, 23:] == 7.0).all() and (vc[:, :, 23:] == -7.0).all()   # nothing past the chunk
+    with pytest.raises(ValueError, match="capacity exceeded"):
+        pkg.kv_cache_append(qkv[:, :18].contiguous().to(cuda), kc, vc, heads, 23)
+
+
+@pytest.mark.parametrize("hd", [8, 16, 32, 64, 128, 256])
+@pytest.mark.parametrize("start,chunk", [(0, 1), (1, 1), (63, 1), (64, 5), (200, 16), (37, 17), (130, 100), (0, 70)])
+def test_attention_kv_cache(pkg, cuda, hd, start, chunk):
+    """Queries at positions start.. over the cached prefix == rows of full causal attention."""
+    b, heads = 2, 2 if hd < 256 else 1
+    length = start + chunk
+    qkv_full = torch.randn(b, length, 3 * heads * hd, generator=_gen(hd * 7 + length)).half()
+    kc, vc = _fill_cache(pkg, qkv_full, heads, length + 9, [start, chunk] if start else [chunk], cuda)
+    ref = _attention_reference(qkv_full, heads)[:, start:]
+    out = pkg.attention_kv_cache(qkv_full[:, start:].contiguous().to(cuda), kc, vc, heads, start)
+    assert out.shape == (b, chunk, heads * hd)
+    # FP16 probabilities and FP16 output rounding (as for the causal kernel).
+    torch.testing.assert_close(out.cpu().float(), ref, atol=2e-3, rtol=1e-2)
+
+
+@pytest.mark.parametrize("b,heads,hd,start", [(1, 16, 64, 20000), (3, 2, 128, 5000), (1, 1, 256, 3000), (64, 4, 32, 127)])
+def test_decode_long_cache(pkg, cuda, b, heads, hd, start):
+    """One new token over a long cache: many key splits merged by the combine kernel."""
+    length = start + 1
+    qkv_full = torch.randn(b, length, 3 * heads * hd, generator=_gen(start)).half()
+    kc, vc = _fill_cache(pkg, qkv_full, heads, length, [start, 1], cuda)
+    q_last = qkv_full[:, start:].contiguous()
+    t = qkv_full.float().view(b, length, 3, heads, hd)
+    scores = torch.einsum("bhd,bkhd->bhk", t[:, start, 0], t[:, :, 1]) * hd**-0.5
+    ref = torch.einsum("bhk,bkhd->bhd", torch.softmax(scores, -1), t[:, :, 2]).reshape(b, 1, heads * hd)
+    need = pkg.kernels.kv_cache_workspace_bytes(b, 1, heads, hd, start)
+    assert need > 0
+    out = pkg.attention_kv_cache(q_last.to(cuda), kc, vc, heads, start)
+    torch.testing.assert_close(out.cpu().float(), ref, atol=2e-3, rtol=1e-2)
+
+
+def test_decode_workspace_too_small(pkg, cuda):
+    b, heads, hd, start = 1, 2, 64, 300
+    qkv_full = torch.randn(b, start + 1, 3 * heads * hd, generator=_gen(3)).half()
+    kc, vc = _fill_cache(pkg, qkv_full, heads, start + 1, [start, 1], cuda)
+    lib = pkg._capi.lib()
+    out = torch.empty(b, 1, heads * hd, device=cuda, dtype=F16)
+    q = qkv_full[:, start:].contiguous().to(cuda)
+    need = pkg.kernels.kv_cache_workspace_bytes(b, 1, heads, hd, start)
+    ws = torch.empty(need, device=cuda, dtype=torch.uint8)
+    code = lib.xb_attention_kv_cache(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), out.data_ptr(), b, 1, heads, hd,
+                                     start, start + 1, 0.125, ws.data_ptr(), need - 16, None)
+    assert code == -7
+    code = lib.xb_attention_kv_cache(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), out.data_ptr(), b, 1, heads, hd,
+                                     start, start + 1, 0.125, None, 0, None)
+    assert code == -1

@@ -296,3 +296,83 @@ def test_mask_argument_errors(pkg, cuda):
         optimized(x, torch.ones(2, 8, dtype=torch.bool))
     with pytest.raises(ValueError):
         optimized(x, torch.ones(2, 8, dtype=torch.float32, device=cuda))
+
+
+# ----------------------------------------------------------------------------- KV-cached decoding
+@pytest.mark.parametrize(
+    "geom,pieces",
+    [
+        ((2, 64, 128, 4, 256, 2), [20] + [1] * 10 + [7, 16, 11]),     # prompt, decode steps, chunks
+        ((3, 40, 1024, 4, 512, 1), [1, 1, 30, 1, 1, 1]),              # head_dim 256, single-token prompt
+        ((2, 50, 128, 16, 128, 2), [17, 1, 1, 31]),                   # head_dim 8
+    ],
+)
+def test_kv_cache_decoding_matches_full_forward(pkg, cuda, geom, pieces):
+    """Step outputs equal the rows of one full causal forward (causality, TTB:747-765)."""
+    config = pkg.TransformerConfig(*geom, True)
+    baseline, optimized = _models(pkg, config, cuda)
+    total = sum(pieces)
+    x = torch.randn(config.batch_size, total, config.d_model, generator=torch.Generator().manual_seed(41))
+    with torch.inference_mode():
+        ref = baseline(x)
+    optimized.enable_kv_cache(True)
+    start = 0
+    with torch.inference_mode():
+        for n in pieces:
+            out = optimized(x[:, start:start + n].to(cuda)).cpu()
+            assert optimized.kv_cache_length == start + n
+            _check(ref[:, start:start + n], out, f"kv cache {geom} positions {start}..{start + n - 1}")
+            start += n
+    optimized.reset_kv_cache()
+    assert optimized.kv_cache_length == 0
+    with torch.inference_mode():  # a new sequence after the reset
+        out = optimized(x[:, :5].to(cuda)).cpu()
+    _check(ref[:, :5], out, "after reset")
+
+
+def test_kv_cache_long_context_decode(pkg, cuda):
+    """A 4000-token prompt, then single tokens: the split-key decode path over a long cache."""
+    config = pkg.TransformerConfig(1, 4100, 256, 4, 256, 2, True)
+    baseline, optimized = _models(pkg, config, cuda)
+    x = torch.randn(1, 4004, 256, generator=torch.Generator().manual_seed(43))
+    with torch.inference_mode():
+        ref = baseline(x)
+    optimized.enable_kv_cache(True)
+    with torch.inference_mode():
+        _check(ref[:, :4000], optimized(x[:, :4000].to(cuda)).cpu(), "prompt 4000")
+        for p in range(4000, 4004):
+            _check(ref[:, p:p + 1], optimized(x[:, p:p + 1].to(cuda)).cpu(), f"decode position {p}")
+
+
+def test_kv_cache_contract(pkg, cuda):
+    config = pkg.TransformerConfig(2, 8, 64, 4, 64, 1, True)
+    _, optimized = _models(pkg, config, cuda)
+    optimized.enable_kv_cache(True)
+    x = torch.randn(2, 6, 64, device=cuda)
+    with torch.inference_mode():
+        optimized(x)
+        with pytest.raises(ValueError, match="capacity exceeded"):
+            optimized(x[:, :3].contiguous())
+        assert optimized.kv_cache_length == 6                 # a refused step changes nothing
+        with pytest.raises(RuntimeError, match="reset it"):
+            optimized(torch.randn(1, 1, 64, device=cuda))     # another batch size
+        mask = torch.ones(2, 1, dtype=torch.bool, device=cuda)
+        mask[0, 0] = False
+        with pytest.raises(ValueError, match="padding"):
+            optimized(x[:, :1].contiguous(), mask)
+        optimized(x[:, :2].contiguous(), torch.ones(2, 2, dtype=torch.bool, device=cuda))  # all-valid mask is fine
+    assert optimized.kv_cache_length == 8
+    with pytest.raises(RuntimeError, match="reset the KV cache"):
+        optimized.enable_mixed_precision(torch.float16)
+    optimized.enable_kv_cache(False)
+    assert optimized.kv_cache_length == 0
+    _, graphs = pkg.UserOptimizedTransformer, __import__(pkg.__name__ + ".graph_runner", fromlist=["x"])
+    optimized.enable_kv_cache(True)
+    model, graphed, reason = graphs.maybe_cuda_graph(optimized, x, None, enabled=True)
+    assert model is optimized and not graphed and "KV-cache" in reason
+    non_causal = pkg.UserOptimizedTransformer(pkg.TransformerConfig(2, 8, 64, 4, 64, 1, False)).to(cuda).eval()
+    with pytest.raises(ValueError, match="causal"):
+        non_causal.enable_kv_cache(True)
+    training = pkg.UserOptimizedTransformer(config).to(cuda)
+    with pytest.raises(RuntimeError, match="eval"):
+        training.enable_kv_cache(True)
