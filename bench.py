@@ -53,6 +53,7 @@ def parse_args():
     p.add_argument("--copy-calibration", action="store_true",
                    help="with --profile-only: also run a plain 1 GiB elementwise copy (HBM counter calibration)")
     p.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 FETCH_SIZE/WRITE_SIZE runs")
+    p.add_argument("--no-decode", action="store_true", help="skip the KV-cache decode measurement")
     p.add_argument("--rounds", type=int, default=1, help="headline: median ms over this many timed rounds of --steps")
     p.add_argument("--batch", type=int, default=0,
                    help="run the headline with this batch instead of the shape's (the line then says so)")
@@ -170,6 +171,69 @@ def measure_traffic(workload: int, dominant: str, batch: int = 0):
                            "bytes": statistics.median(kernel_vals) * factor, "dispatches": len(kernel_vals)}
     total = detail["FETCH_SIZE"]["bytes"] + detail["WRITE_SIZE"]["bytes"]
     return total, detail
+
+
+DECODE_CONFIG = (32, 100000, 1024, 16, 1024, 2)   # cfg5's geometry; the cache holds seq_len tokens
+DECODE_SPARE = 16                                  # cache slots left for the decode steps
+
+
+def decode_leg(pkg, kernels, device, time_steps):
+    """KV-cached decoding at cfg5's geometry: B=32 caches of 99,984 tokens, one new token per step.
+
+    A step is one forward of [32, 1, 1024] with the cache enabled; its cost is
+    dominated by the split-key attention reading each layer's K/V cache
+    (4*B*S_k*D bytes per layer).  The first step's output is checked against
+    the uncached forward's row at the same position (the reference's rule,
+    computed here), i.e. the flash path's causal attention.
+    """
+    import torch
+
+    cfg = pkg.TransformerConfig(*DECODE_CONFIG, True)
+    torch.manual_seed(1234)
+    model = pkg.UserOptimizedTransformer(cfg).to(device).eval()
+    prompt = cfg.seq_len - DECODE_SPARE
+    g = torch.Generator(device=device).manual_seed(1234 + 200000)
+    x_all = torch.randn(cfg.batch_size, prompt + 1, cfg.d_model, generator=g, device=device)
+    log(f"[bench] decode: {cfg}, prompt {prompt} tokens in the cache, single-token steps")
+    model.enable_kv_cache(True)
+    with torch.inference_mode():
+        model(x_all[:, :prompt])
+        first = model(x_all[:, prompt:]).clone()
+        token = x_all[:, prompt:].clone()
+        ms, _ = time_steps(lambda: model(token), 8, 1)
+        steps = 4
+        with kernels.LaunchRecorder() as rec:
+            for _ in range(steps):
+                model(token)
+        torch.cuda.synchronize()
+        length = model.kv_cache_length
+        model.enable_kv_cache(False)
+        full = model(x_all)[:, prompt:]
+        torch.cuda.synchronize()
+    diff = (first - full).abs()
+    failed = int(((diff > 2e-3) & (diff > 0.02 * full.abs())).sum().item()) + int((~torch.isfinite(first)).sum().item())
+    per = {}
+    for name, durs in rec.durations_ms().items():
+        per[name] = {"avg_us": round(statistics.fmean(durs) * 1e3, 2), "per_step": len(durs) // steps}
+    attn = next((k for k in per if k.startswith("attention_kv") and k.endswith("_decode")), None)
+    out = {
+        "workload": f"cfg5 geometry decode: B={cfg.batch_size}, cache {prompt}..{length} tokens, D={cfg.d_model}, "
+                    f"H={cfg.num_heads}, L={cfg.num_layers}, one token per sequence per step",
+        "ms_per_step": ms, "tokens_per_s": cfg.batch_size / (ms / 1e3),
+        "check_vs_uncached_forward": {"failed": failed, "total": first.numel(), "max_abs": float(diff.max().item())},
+        "kernels": per,
+    }
+    if attn is not None:
+        s_k = length - steps // 2  # mean cache length over the recorded steps
+        by = 4.0 * cfg.batch_size * s_k * cfg.d_model  # K and V rows, FP16, read once
+        sec = per[attn]["avg_us"] / 1e6
+        out["roofline"] = {"kernel": attn, "bound": "hbm", "achieved": by / sec / 1e9, "peak": HBM_BYTES_PER_S / 1e9,
+                           "unit": "GB/s", "frac": by / sec / HBM_BYTES_PER_S, "bytes_per_launch": by}
+        log(f"[bench] decode: {ms:.3f} ms/step, {out['tokens_per_s']:.4g} tokens/s; {attn} {per[attn]['avg_us']:.1f} us "
+            f"= {by / sec / 1e9:.0f} GB/s ({by / sec / HBM_BYTES_PER_S * 100:.1f}% of HBM); check failed={failed}")
+    del model, x_all
+    torch.cuda.empty_cache()
+    return out
 
 
 def main() -> int:
@@ -369,6 +433,10 @@ def main() -> int:
         del baseline, model, x, out
         torch.cuda.empty_cache()
 
+    decode = None
+    if not (args.no_per_config or args.profile_only or args.no_decode):
+        decode = decode_leg(pkg, kernels, device, time_steps)
+
     if args.profile_only and args.copy_calibration:
         # A plain streaming copy of known size: reads and writes exactly
         # CALIBRATION_BYTES (the HBM counters' scale reference).
@@ -426,6 +494,8 @@ def main() -> int:
     if "cpu_baseline" in headline:
         line["cpu_baseline"] = headline["cpu_baseline"]
         line["accuracy"] = headline["accuracy"]
+    if decode is not None:
+        line["decode"] = decode
     if len(results) > 1:
         line["per_config"] = {n: {k: (round(v, 6) if isinstance(v, float) else v) for k, v in r.items()} for n, r in results.items()}
     print(json.dumps(line), flush=True)
