@@ -406,6 +406,406 @@ __global__ __launch_bounds__(64 * NW, 1) void fused_stack_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Sixteen-wave variant (head_dim <= 64).  Each token block is shared by two
+// waves that split every product's OUTPUT features: wave half h owns feature
+// blocks 4h .. 4h+3, which are k-steps 2h, 2h+1 of the next product's operand
+// and the heads inside them.  Four waves per SIMD instead of two hide the
+// MFMA -> softmax / GELU / LayerNorm -> MFMA dependency chains; the price is
+// an LDS exchange of operand halves (LayerNorm outputs, attention context,
+// FFN hidden) and of LayerNorm partial statistics between the two waves of a
+// block.  The exchanges reuse the K and V^T areas while those are dead.
+namespace w16 {
+
+constexpr int NW = 16;
+constexpr int OB = FB / 2;  // own output feature blocks
+constexpr int OK = KS / 2;  // own k-steps
+static_assert(P_LAYER * 4 == NW * 20 * 16, "layer vectors: 20 lanes x 16 bytes per wave");
+static_assert(2 * D * 4 == NW * 4 * 16, "final LayerNorm vectors: 4 lanes x 16 bytes per wave");
+static_assert(8 * 2 * OK * 1024 <= SMAX * LD * 2, "an exchange area fits in the K (or V^T) area");
+
+// a[j] += staged-matrix output block (OB*half + j) times the operands act.
+template <bool SWAP>
+__device__ __forceinline__ void stage_gemm_half(const char* st, const half8_t (&act)[KS], float4_t (&a)[OB], int half,
+                                                int lane) {
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    half8_t f[OB];
+#pragma unroll
+    for (int j = 0; j < OB; ++j) f[j] = sfrag(st, (OB * half + j) * KS + ks, lane);
+#pragma unroll
+    for (int j = 0; j < OB; ++j)
+      a[j] = SWAP ? mfma16x16x32(f[j], act[ks], a[j]) : mfma16x16x32(act[ks], f[j], a[j]);
+  }
+}
+
+// Workgroup barrier over LDS traffic only: the weight DMA may stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // vmcnt(63) expcnt(7) lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Mean and rstd of the block's rows from both halves: each wave's (mean, M2)
+// over its 64 features meet in LDS and merge by Chan's pairwise formula
+// (equal counts: M2 = M2a + M2b + (ma - mb)^2 * 32).  Both waves of a pair get
+// bit-identical results (the merge is symmetric).
+__device__ __forceinline__ void split_row_stats(const float4_t (&r)[OB], float2* xs, int wave, int lane, float& mean,
+                                                float& rstd) {
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < OB; ++j) s += (r[j][0] + r[j][1]) + (r[j][2] + r[j][3]);
+  const float ma = quad_group_sum(s) * (1.0f / 64);
+  float q = 0.f;
+#pragma unroll
+  for (int j = 0; j < OB; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { const float c = r[j][i] - ma; q += c * c; }
+  const float m2a = quad_group_sum(q);
+  if (lane < 16) xs[wave * 16 + lane] = make_float2(ma, m2a);
+  lds_barrier();
+  const float2 pb = xs[(wave ^ 8) * 16 + lane % 16];
+  const float d = pb.x - ma;
+  mean = 0.5f * (ma + pb.x);
+  rstd = __builtin_amdgcn_rsqf(((m2a + pb.y) + d * d * 32.f) * (1.0f / D) + 1e-5f);
+}
+
+// LayerNorm of the wave's half of the block -> its two k-steps of operand.
+__device__ __forceinline__ void split_layer_norm(const float4_t (&res)[OB], const float* gamma, const float* beta,
+                                                 float2* xs, int wave, int lane, int half, int g,
+                                                 half8_t (&own)[OK]) {
+  float mean, rstd;
+  split_row_stats(res, xs, wave, lane, mean, rstd);
+  const float shift = -mean * rstd;
+#pragma unroll
+  for (int j = 0; j < OK; ++j) {
+    const int ks = OK * half + j;
+    float4_t lo, hi;
+    const float4_t g0 = ld4(gamma + 32 * ks + 4 * g), g1 = ld4(gamma + 32 * ks + 16 + 4 * g);
+    const float4_t b0 = ld4(beta + 32 * ks + 4 * g), b1 = ld4(beta + 32 * ks + 16 + 4 * g);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      lo[i] = fmaf(fmaf(res[2 * j][i], rstd, shift), g0[i], b0[i]);
+      hi[i] = fmaf(fmaf(res[2 * j + 1][i], rstd, shift), g1[i], b1[i]);
+    }
+    own[j] = to_operand(lo, hi);
+  }
+}
+
+// Exchange slot of (token block, half, k-step): 1 KB, 16 bytes per lane.
+__device__ __forceinline__ half8_t* xslot(char* area, int tb, int half, int j, int lane) {
+  return reinterpret_cast<half8_t*>(area + ((tb * 2 + half) * OK + j) * 1024 + lane * 16);
+}
+__device__ __forceinline__ void put_half(char* area, const half8_t (&own)[OK], half8_t (&full)[KS], int tb, int half,
+                                         int lane) {
+#pragma unroll
+  for (int j = 0; j < OK; ++j) {
+    *xslot(area, tb, half, j, lane) = own[j];
+    full[OK * half + j] = own[j];
+  }
+}
+// After a barrier that follows the partner's put_half.
+__device__ __forceinline__ void get_partner(char* area, half8_t (&full)[KS], int tb, int half, int lane) {
+#pragma unroll
+  for (int j = 0; j < OK; ++j) full[OK * (half ^ 1) + j] = *xslot(area, tb, half ^ 1, j, lane);
+}
+
+struct Lds {
+  half_t k[SMAX * LD];                                 // K, or an exchange area
+  half_t vt[D * LD];                                   // V^T, or an exchange area
+  __attribute__((aligned(1024))) char wst[2][MAT_BYTES];  // weight matrix stages
+  float prm[2][P_LAYER];                               // per-layer vectors, by layer parity
+  float2 xstat[2][NW * 16];                            // LayerNorm partial statistics
+};
+
+// The kernel body for one half (HALF is a compile-time constant so that every
+// register-array index below is static).
+template <int HD, int HALF>
+__device__ __forceinline__ void stack16_body(Lds& L, const float* __restrict__ x, float* __restrict__ y,
+                                             const half_t* __restrict__ wpack, const float* __restrict__ ppack,
+                                             int S, int layers, int wave, int tb) {
+  constexpr int H = D / HD;
+  static_assert(H >= 2, "heads split between the two halves");
+  constexpr int HH = H / 2;                    // heads per half
+  constexpr int HDB = HD < 16 ? 1 : HD / 16;   // 16-row blocks of one head in V^T
+  constexpr int KSH = HD >= 32 ? HD / 32 : 1;  // k-steps of one head's q.k
+  constexpr int half = HALF;
+  half_t* const k_lds = L.k;
+  half_t* const vt_lds = L.vt;
+  auto& wst = L.wst;
+  auto& prm = L.prm;
+  auto& xstat = L.xstat;
+  char* const area_a = reinterpret_cast<char*>(k_lds);
+  char* const area_b = reinterpret_cast<char*>(vt_lds);
+
+  const int lane = threadIdx.x % kWave;
+  const int g = lane / 16, r16 = lane % 16;
+  float4_t diag_mask;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) diag_mask[i] = (4 * g + i > r16) ? -INFINITY : 0.f;
+  const int64_t seq = blockIdx.x;
+  const float* xs = x + seq * S * D;
+  float* ys = y + seq * S * D;
+  const int groups = layers * MATS;
+
+  auto issue_group = [&](int gi) {
+    const int layer = gi / MATS, m = gi % MATS;
+    const half_t* src = wpack + ((int64_t)layer * MATS + m) * MAT_FRAGS * 512;
+#pragma unroll
+    for (int j = 0; j < MAT_FRAGS / NW; ++j) {
+      const int f = wave + NW * j;
+      dma16(src + (f * 64 + lane) * 8, wst[gi & 1] + f * 1024);
+    }
+    if (m == MATS - 1) {
+      float* dst = prm[(layer + 1) & 1];
+      if (layer + 1 < layers) {
+        if (lane < 20) dma16(ppack + (int64_t)(layer + 1) * P_LAYER + wave * 80 + lane * 4, dst + wave * 80);
+      } else {
+        if (lane < 4) dma16(ppack + (int64_t)layers * P_LAYER + wave * 16 + lane * 4, dst + wave * 16);
+      }
+    }
+  };
+  auto begin_group = [&](int gi) -> const char* {
+    drain_and_barrier();
+    if (gi + 1 < groups) issue_group(gi + 1);
+    return wst[gi & 1];
+  };
+
+  // Residual stream, own half: res[j][i] = x[16 tb + r16][16 (OB half + j) + 4 g + i].
+  float4_t res[OB];
+  const int tok = 16 * tb + r16;
+#pragma unroll
+  for (int j = 0; j < OB; ++j)
+    res[j] = tok < S ? ld4(xs + (int64_t)tok * D + 16 * (OB * half + j) + 4 * g) : float4_t{0.f, 0.f, 0.f, 0.f};
+  if (lane < 20) dma16(ppack + wave * 80 + lane * 4, prm[0] + wave * 80);
+  issue_group(0);
+  drain_and_barrier();
+
+  for (int layer = 0; layer < layers; ++layer) {
+    const float* pp = prm[layer & 1];
+    const int g0 = layer * MATS;
+    half8_t xn[KS];
+    {
+      half8_t own[OK];
+      split_layer_norm(res, pp + P_G1, pp + P_BE1, xstat[0], wave, lane, half, g, own);
+      put_half(area_a, own, xn, tb, half, lane);
+    }
+
+    // ---- Q (own heads), kept in registers --------------------------------
+    half8_t qop[OK];
+    {
+      const char* st = begin_group(g0 + 0);
+      get_partner(area_a, xn, tb, half, lane);
+      float4_t qc[OB];
+#pragma unroll
+      for (int j = 0; j < OB; ++j) qc[j] = ld4(pp + P_BQ + 16 * (OB * half + j) + 4 * g);
+      stage_gemm_half<true>(st, xn, qc, half, lane);
+#pragma unroll
+      for (int j = 0; j < OK; ++j) qop[j] = to_operand(qc[2 * j], qc[2 * j + 1]);
+    }
+    // ---- K (own features) -> LDS, permuted per k-step ----------------------
+    {
+      const char* st = begin_group(g0 + 1);
+      float4_t a[OB];
+#pragma unroll
+      for (int j = 0; j < OB; ++j) a[j] = ld4(pp + P_BK + 16 * (OB * half + j) + 4 * g);
+      stage_gemm_half<true>(st, xn, a, half, lane);
+#pragma unroll
+      for (int j = 0; j < OB; ++j) {
+        const int ob = OB * half + j;
+        *reinterpret_cast<half4_t*>(k_lds + (16 * tb + r16) * LD + 32 * (ob / 2) + 8 * g + 4 * (ob & 1)) =
+            to_half4(a[j]);
+      }
+    }
+    // ---- V (own features) -> V^T in LDS -------------------------------------
+    {
+      const char* st = begin_group(g0 + 2);
+      float4_t a[OB];
+#pragma unroll
+      for (int j = 0; j < OB; ++j) {
+        const float bv = pp[P_BV + 16 * (OB * half + j) + r16];
+        a[j] = float4_t{bv, bv, bv, bv};
+      }
+      stage_gemm_half<false>(st, xn, a, half, lane);
+#pragma unroll
+      for (int j = 0; j < OB; ++j)
+        *reinterpret_cast<half4_t*>(vt_lds + (16 * (OB * half + j) + r16) * LD + 16 * tb + 4 * g) = to_half4(a[j]);
+    }
+    lds_barrier();  // K and V^T of every token block are in LDS
+
+    // ---- causal attention of the block's queries, own heads -----------------
+    const int qb = tb;
+    half8_t cop[KS];
+#pragma unroll
+    for (int j = 0; j < OK; ++j) cop[OK * half + j] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int hh = 0; hh < HH; ++hh) {
+      const int h = HH * half + hh;
+      // An opaque per-head copy: otherwise the compiler hoists the eight
+      // "kb == qb ? mask : -0" selects out of the layer loop and spills them.
+      float4_t dm = diag_mask;
+      asm volatile("" : "+v"(dm));
+      const int ks0 = (h * HD) / 32;
+      half8_t qh[KSH];
+#pragma unroll
+      for (int j = 0; j < KSH; ++j) {
+        qh[j] = qop[ks0 + j - OK * half];
+        if constexpr (HD < 32) {  // keep only this head's features of the shared k-step
+#pragma unroll
+          for (int m = 0; m < 8; ++m)
+            if ((32 * ks0 + 4 * g + (m & 3) + 16 * (m >> 2)) / HD != h) qh[j][m] = (half_t)0.f;
+        }
+      }
+      float4_t sc[8];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 8; ++kb) {
+        sc[kb] = float4_t{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        if (kb <= qb) {
+          float4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int j = 0; j < KSH; ++j) {
+            const half8_t kf = *reinterpret_cast<const half8_t*>(k_lds + (16 * kb + r16) * LD + 32 * (ks0 + j) + 8 * g);
+            acc = mfma16x16x32(kf, qh[j], acc);
+          }
+          if (kb == qb) acc += dm;
+          sc[kb] = acc;
+          mx = fmaxf(mx, fmaxf(fmaxf(acc[0], acc[1]), fmaxf(acc[2], acc[3])));
+        }
+      }
+      mx = quad_group_max(mx);
+      const half8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
+      float4_t lacc = {0.f, 0.f, 0.f, 0.f};
+      const int vrow0 = HD < 16 ? 16 * (h / 2) : h * HD;
+      float4_t o[HDB];
+#pragma unroll
+      for (int hb = 0; hb < HDB; ++hb) o[hb] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        if (2 * kt <= qb) {
+          float4_t p0, p1;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            p0[i] = __builtin_amdgcn_exp2f(sc[2 * kt][i] - mx);
+            p1[i] = __builtin_amdgcn_exp2f(sc[2 * kt + 1][i] - mx);
+          }
+          const half8_t pf = to_operand(p0, p1);
+          lacc = mfma16x16x32(ones, pf, lacc);
+#pragma unroll
+          for (int hb = 0; hb < HDB; ++hb) {
+            const half_t* vr = vt_lds + (vrow0 + 16 * hb + r16) * LD + 32 * kt + 4 * g;
+            const half8_t vf = cat4(*reinterpret_cast<const half4_t*>(vr), *reinterpret_cast<const half4_t*>(vr + 16));
+            o[hb] = mfma16x16x32(vf, pf, o[hb]);
+          }
+        }
+      }
+      const float inv = __builtin_amdgcn_rcpf(lacc[0]);
+      if constexpr (HD >= 16) {
+#pragma unroll
+        for (int hb = 0; hb < HDB; ++hb) {
+          const int c = (vrow0 + 16 * hb) / 16;
+          const half4_t v = to_half4(o[hb] * inv);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) cop[c / 2][4 * (c & 1) + i] = v[i];
+        }
+      } else {
+        const int c = vrow0 / 16;
+        if ((g / 2) == (h & 1)) {
+          const half4_t v = to_half4(o[0] * inv);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) cop[c / 2][4 * (c & 1) + i] = v[i];
+        }
+      }
+    }
+    lds_barrier();  // every wave is done with K and V^T: their areas take exchanges now
+    {
+      half8_t own[OK];
+#pragma unroll
+      for (int j = 0; j < OK; ++j) own[j] = cop[OK * half + j];
+      put_half(area_b, own, cop, tb, half, lane);
+    }
+
+    // ---- output projection + residual (own features) ------------------------
+    {
+      const char* st = begin_group(g0 + 3);
+      get_partner(area_b, cop, tb, half, lane);
+      float4_t a[OB];
+#pragma unroll
+      for (int j = 0; j < OB; ++j) a[j] = ld4(pp + P_BO + 16 * (OB * half + j) + 4 * g);
+      stage_gemm_half<true>(st, cop, a, half, lane);
+#pragma unroll
+      for (int j = 0; j < OB; ++j) res[j] += a[j];
+    }
+
+    // ---- LN2, FFN -------------------------------------------------------------
+    {
+      half8_t own[OK];
+      split_layer_norm(res, pp + P_G2, pp + P_BE2, xstat[1], wave, lane, half, g, own);
+      put_half(area_a, own, xn, tb, half, lane);
+    }
+    half8_t hf[KS];
+    {
+      const char* st = begin_group(g0 + 4);
+      get_partner(area_a, xn, tb, half, lane);
+      float4_t a[OB];
+#pragma unroll
+      for (int j = 0; j < OB; ++j) a[j] = ld4(pp + P_B1 + 16 * (OB * half + j) + 4 * g);
+      stage_gemm_half<true>(st, xn, a, half, lane);
+      half8_t own[OK];
+#pragma unroll
+      for (int j = 0; j < OB; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) own[j / 2][(j & 1) * 4 + i] = (half_t)gelu_erf(a[j][i]);
+      put_half(area_b, own, hf, tb, half, lane);
+    }
+    {
+      const char* st = begin_group(g0 + 5);
+      get_partner(area_b, hf, tb, half, lane);
+      float4_t a[OB];
+#pragma unroll
+      for (int j = 0; j < OB; ++j) a[j] = ld4(pp + P_B2 + 16 * (OB * half + j) + 4 * g);
+      stage_gemm_half<true>(st, hf, a, half, lane);
+#pragma unroll
+      for (int j = 0; j < OB; ++j) res[j] += a[j];
+    }
+  }
+
+  // ---- final LayerNorm, FP32 output, own features ------------------------------
+  drain_and_barrier();
+  const float* gf = prm[layers & 1];
+  const float* bf = gf + D;
+  float mean, rstd;
+  split_row_stats(res, xstat[0], wave, lane, mean, rstd);
+  if (tok < S) {
+#pragma unroll
+    for (int j = 0; j < OB; ++j) {
+      const int f0 = 16 * (OB * half + j) + 4 * g;
+      const float4_t gg = ld4(gf + f0), bb = ld4(bf + f0);
+      float4_t o;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = (res[j][i] - mean) * rstd * gg[i] + bb[i];
+      *reinterpret_cast<float4_t*>(ys + (int64_t)tok * D + f0) = o;
+    }
+  }
+}
+
+template <int HD>
+__global__ __launch_bounds__(64 * NW, 1) void fused_stack16_kernel(
+    const float* __restrict__ x, float* __restrict__ y, const half_t* __restrict__ wpack,
+    const float* __restrict__ ppack, int S, int layers) {
+  __shared__ Lds lds;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int wi = wave % 8;
+  const int tb = wi < 4 ? wi : 11 - wi;  // the four waves of a SIMD hold blocks b, 7-b (both halves)
+  if (wave < 8)
+    stack16_body<HD, 0>(lds, x, y, wpack, ppack, S, layers, wave, tb);
+  else
+    stack16_body<HD, 1>(lds, x, y, wpack, ppack, S, layers, wave, tb);
+}
+
+}  // namespace w16
+
 // Fragment-major FP16 packing of an nn.Linear weight [n, k] (FP32 source).
 // permuted: k index 32ks + 4(l/16) + (m&3) + 16(m>>2); natural: 32ks + 8(l/16) + m.
 __global__ void pack_fragments_kernel(const float* __restrict__ w, half_t* __restrict__ out, int n, int k,
@@ -432,7 +832,12 @@ __global__ void pack_fragments_kernel(const float* __restrict__ w, half_t* __res
 template <int HD>
 static hipError_t launch(const float* x, float* y, const half_t* w, const float* p, int64_t batch, int S,
                          int layers, hipStream_t s) {
-  hipLaunchKernelGGL((fused_stack_kernel<HD>), dim3((unsigned)batch), dim3(64 * NW), 0, s, x, y, w, p, S, layers);
+  if constexpr (HD <= 64) {
+    hipLaunchKernelGGL((w16::fused_stack16_kernel<HD>), dim3((unsigned)batch), dim3(64 * w16::NW), 0, s, x, y, w, p,
+                       S, layers);
+  } else {
+    hipLaunchKernelGGL((fused_stack_kernel<HD>), dim3((unsigned)batch), dim3(64 * NW), 0, s, x, y, w, p, S, layers);
+  }
   return hipGetLastError();
 }
 
