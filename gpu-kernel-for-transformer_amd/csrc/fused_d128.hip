@@ -519,6 +519,95 @@ struct Lds {
   float2 xstat[2][NW * 16];                            // LayerNorm partial statistics
 };
 
+// Causal attention of query block QB (keys 0 .. 16 QB + 15) for the heads of
+// half HALF.  S^T = K . Q^T (M = keys, N = queries): lane holds keys
+// 16kb + 4g + i of query r16, which with the key order 32kt + 4g + (m&3) +
+// 16(m>>2) is the B operand of O^T = V^T . P^T directly.  All scores of a
+// query fit in registers, so the softmax needs no running rescale; row sums
+// come from an all-ones A operand.  The context leaves as MFMA operands in
+// the permuted k order (cop, own k-steps only).
+template <int HD, int HALF, int QB>
+__device__ __forceinline__ void attend16(const half_t* k_lds, const half_t* vt_lds, const half8_t (&qop)[OK],
+                                         half8_t (&cop)[KS], const float4_t& diag_mask, int g, int r16) {
+  constexpr int H = D / HD;
+  constexpr int HH = H / 2;
+  constexpr int HDB = HD < 16 ? 1 : HD / 16;
+  constexpr int KSH = HD >= 32 ? HD / 32 : 1;
+  constexpr int NKT = QB / 2 + 1;  // 32-key steps of the PV product
+#pragma unroll
+  for (int hh = 0; hh < HH; ++hh) {
+    const int h = HH * HALF + hh;
+    const int ks0 = (h * HD) / 32;
+    half8_t qh[KSH];
+#pragma unroll
+    for (int j = 0; j < KSH; ++j) {
+      qh[j] = qop[ks0 + j - OK * HALF];
+      if constexpr (HD < 32) {  // keep only this head's features of the shared k-step
+#pragma unroll
+        for (int m = 0; m < 8; ++m)
+          if ((32 * ks0 + 4 * g + (m & 3) + 16 * (m >> 2)) / HD != h) qh[j][m] = (half_t)0.f;
+      }
+    }
+    float4_t sc[QB + 1];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb <= QB; ++kb) {
+      float4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < KSH; ++j) {
+        const half8_t kf = *reinterpret_cast<const half8_t*>(k_lds + (16 * kb + r16) * LD + 32 * (ks0 + j) + 8 * g);
+        acc = mfma16x16x32(kf, qh[j], acc);
+      }
+      if (kb == QB) acc += diag_mask;  // -inf above the diagonal
+      sc[kb] = acc;
+      mx = fmaxf(mx, fmaxf(fmaxf(acc[0], acc[1]), fmaxf(acc[2], acc[3])));
+    }
+    mx = quad_group_max(mx);
+    const half8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
+    float4_t lacc = {0.f, 0.f, 0.f, 0.f};
+    const int vrow0 = HD < 16 ? 16 * (h / 2) : h * HD;
+    float4_t o[HDB];
+#pragma unroll
+    for (int hb = 0; hb < HDB; ++hb) o[hb] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kt = 0; kt < NKT; ++kt) {
+      float4_t p0, p1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p0[i] = __builtin_amdgcn_exp2f(sc[2 * kt][i] - mx);
+      if (2 * kt + 1 <= QB) {  // constant once the loop is unrolled
+#pragma unroll
+        for (int i = 0; i < 4; ++i) p1[i] = __builtin_amdgcn_exp2f(sc[2 * kt + 1][i] - mx);
+      }
+      const half8_t pf = to_operand(p0, p1);
+      lacc = mfma16x16x32(ones, pf, lacc);
+#pragma unroll
+      for (int hb = 0; hb < HDB; ++hb) {
+        const half_t* vr = vt_lds + (vrow0 + 16 * hb + r16) * LD + 32 * kt + 4 * g;
+        const half8_t vf = cat4(*reinterpret_cast<const half4_t*>(vr), *reinterpret_cast<const half4_t*>(vr + 16));
+        o[hb] = mfma16x16x32(vf, pf, o[hb]);
+      }
+    }
+    const float inv = __builtin_amdgcn_rcpf(lacc[0]);
+    if constexpr (HD >= 16) {
+#pragma unroll
+      for (int hb = 0; hb < HDB; ++hb) {
+        const int c = (vrow0 + 16 * hb) / 16;
+        const half4_t v = to_half4(o[hb] * inv);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) cop[c / 2][4 * (c & 1) + i] = v[i];
+      }
+    } else {
+      // Two 8-wide heads share one 16-row block: rows 0-7 (g < 2) are the even head's.
+      const int c = vrow0 / 16;
+      if ((g / 2) == (h & 1)) {
+        const half4_t v = to_half4(o[0] * inv);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) cop[c / 2][4 * (c & 1) + i] = v[i];
+      }
+    }
+  }
+}
+
 // The kernel body for one half (HALF is a compile-time constant so that every
 // register-array index below is static).
 template <int HD, int HALF>
@@ -635,88 +724,21 @@ __device__ __forceinline__ void stack16_body(Lds& L, const float* __restrict__ x
     lds_barrier();  // K and V^T of every token block are in LDS
 
     // ---- causal attention of the block's queries, own heads -----------------
-    const int qb = tb;
+    // One specialisation per query block: with the key-block count known at
+    // compile time the heads' MFMA and softmax work forms one branch-free
+    // stretch the scheduler can interleave.
     half8_t cop[KS];
 #pragma unroll
     for (int j = 0; j < OK; ++j) cop[OK * half + j] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-    for (int hh = 0; hh < HH; ++hh) {
-      const int h = HH * half + hh;
-      // An opaque per-head copy: otherwise the compiler hoists the eight
-      // "kb == qb ? mask : -0" selects out of the layer loop and spills them.
-      float4_t dm = diag_mask;
-      asm volatile("" : "+v"(dm));
-      const int ks0 = (h * HD) / 32;
-      half8_t qh[KSH];
-#pragma unroll
-      for (int j = 0; j < KSH; ++j) {
-        qh[j] = qop[ks0 + j - OK * half];
-        if constexpr (HD < 32) {  // keep only this head's features of the shared k-step
-#pragma unroll
-          for (int m = 0; m < 8; ++m)
-            if ((32 * ks0 + 4 * g + (m & 3) + 16 * (m >> 2)) / HD != h) qh[j][m] = (half_t)0.f;
-        }
-      }
-      float4_t sc[8];
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kb = 0; kb < 8; ++kb) {
-        sc[kb] = float4_t{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-        if (kb <= qb) {
-          float4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int j = 0; j < KSH; ++j) {
-            const half8_t kf = *reinterpret_cast<const half8_t*>(k_lds + (16 * kb + r16) * LD + 32 * (ks0 + j) + 8 * g);
-            acc = mfma16x16x32(kf, qh[j], acc);
-          }
-          if (kb == qb) acc += dm;
-          sc[kb] = acc;
-          mx = fmaxf(mx, fmaxf(fmaxf(acc[0], acc[1]), fmaxf(acc[2], acc[3])));
-        }
-      }
-      mx = quad_group_max(mx);
-      const half8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
-      float4_t lacc = {0.f, 0.f, 0.f, 0.f};
-      const int vrow0 = HD < 16 ? 16 * (h / 2) : h * HD;
-      float4_t o[HDB];
-#pragma unroll
-      for (int hb = 0; hb < HDB; ++hb) o[hb] = float4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        if (2 * kt <= qb) {
-          float4_t p0, p1;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            p0[i] = __builtin_amdgcn_exp2f(sc[2 * kt][i] - mx);
-            p1[i] = __builtin_amdgcn_exp2f(sc[2 * kt + 1][i] - mx);
-          }
-          const half8_t pf = to_operand(p0, p1);
-          lacc = mfma16x16x32(ones, pf, lacc);
-#pragma unroll
-          for (int hb = 0; hb < HDB; ++hb) {
-            const half_t* vr = vt_lds + (vrow0 + 16 * hb + r16) * LD + 32 * kt + 4 * g;
-            const half8_t vf = cat4(*reinterpret_cast<const half4_t*>(vr), *reinterpret_cast<const half4_t*>(vr + 16));
-            o[hb] = mfma16x16x32(vf, pf, o[hb]);
-          }
-        }
-      }
-      const float inv = __builtin_amdgcn_rcpf(lacc[0]);
-      if constexpr (HD >= 16) {
-#pragma unroll
-        for (int hb = 0; hb < HDB; ++hb) {
-          const int c = (vrow0 + 16 * hb) / 16;
-          const half4_t v = to_half4(o[hb] * inv);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) cop[c / 2][4 * (c & 1) + i] = v[i];
-        }
-      } else {
-        const int c = vrow0 / 16;
-        if ((g / 2) == (h & 1)) {
-          const half4_t v = to_half4(o[0] * inv);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) cop[c / 2][4 * (c & 1) + i] = v[i];
-        }
-      }
+    switch (tb) {
+      case 0: attend16<HD, HALF, 0>(k_lds, vt_lds, qop, cop, diag_mask, g, r16); break;
+      case 1: attend16<HD, HALF, 1>(k_lds, vt_lds, qop, cop, diag_mask, g, r16); break;
+      case 2: attend16<HD, HALF, 2>(k_lds, vt_lds, qop, cop, diag_mask, g, r16); break;
+      case 3: attend16<HD, HALF, 3>(k_lds, vt_lds, qop, cop, diag_mask, g, r16); break;
+      case 4: attend16<HD, HALF, 4>(k_lds, vt_lds, qop, cop, diag_mask, g, r16); break;
+      case 5: attend16<HD, HALF, 5>(k_lds, vt_lds, qop, cop, diag_mask, g, r16); break;
+      case 6: attend16<HD, HALF, 6>(k_lds, vt_lds, qop, cop, diag_mask, g, r16); break;
+      default: attend16<HD, HALF, 7>(k_lds, vt_lds, qop, cop, diag_mask, g, r16); break;
     }
     lds_barrier();  // every wave is done with K and V^T: their areas take exchanges now
     {
