@@ -134,6 +134,10 @@ class UserOptimizedTransformer(nn.Module):
         self._kv_cache_length = 0
         self._large_batch_chunk_size = self._shape_execution_plan.batch_chunk_size
         self._fused_stack_enabled = True
+        # Recorded for the reference's toggles (TTB:379-406); see their methods.
+        self._triton_fused_norm_enabled = True
+        self._triton_fused_ffn_enabled = True
+        self._attention_fp16_accumulation_enabled = False
 
     # ----------------------------------------------------------------- toggles
     @property
@@ -148,6 +152,30 @@ class UserOptimizedTransformer(nn.Module):
         if self._kv_cache_length:
             raise RuntimeError("reset the KV cache before changing precision")
         self._mixed_precision_dtype = dtype
+
+    def enable_triton_fused_norm(self, enabled: bool = True) -> None:
+        """Accepted for the reference's API (TTB:379-385); the gfx950 path has no Triton.
+
+        Its residual-add + LayerNorm is always one HIP kernel (or part of the
+        whole-stack kernel), so the flag is recorded and changes nothing.
+        """
+        self._triton_fused_norm_enabled = bool(enabled)
+
+    def enable_triton_fused_ffn(self, enabled: bool = True) -> None:
+        """Accepted for the reference's API (TTB:387-393); the FFN GEMM always carries its GELU epilogue."""
+        self._triton_fused_ffn_enabled = bool(enabled)
+
+    def enable_attention_fp16_accumulation(self, enabled: bool = True) -> None:
+        """The reference's switch (TTB:395-406), same refusal for causal models.
+
+        MFMA accumulates in FP32 at full rate, so on gfx950 the attention
+        never accumulates in FP16; for a non-causal model the flag is recorded
+        and changes nothing.
+        """
+        if enabled and self.config.causal:
+            raise ValueError(
+                "FP16 attention accumulation is disabled for causal models because it exceeds the accuracy tolerance")
+        self._attention_fp16_accumulation_enabled = bool(enabled)
 
     def enable_fused_stack(self, enabled: bool = True) -> None:
         """Use the one-kernel whole-stack forward where its shape contract holds.

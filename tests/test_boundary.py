@@ -87,6 +87,13 @@ def test_toggles(pkg):
     with pytest.raises(ValueError, match="causal"):
         pkg.UserOptimizedTransformer(pkg.TransformerConfig(1, 4, 32, 4, 32, 1, False)).eval().enable_kv_cache(True)
     assert model.shape_execution_plan.official_shape_id is None
+    # The reference's main() toggles (TTB:1765-1770) are accepted.
+    model.enable_triton_fused_norm(False)
+    model.enable_triton_fused_ffn(False)
+    model.enable_attention_fp16_accumulation(False)
+    with pytest.raises(ValueError, match="causal"):
+        model.enable_attention_fp16_accumulation(True)
+    pkg.UserOptimizedTransformer(pkg.TransformerConfig(1, 4, 32, 4, 32, 1, False)).enable_attention_fp16_accumulation(True)
 
 
 def test_product_never_touches_the_oracle():
