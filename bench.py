@@ -54,6 +54,8 @@ def parse_args():
                    help="with --profile-only: also run a plain 1 GiB elementwise copy (HBM counter calibration)")
     p.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 FETCH_SIZE/WRITE_SIZE runs")
     p.add_argument("--no-decode", action="store_true", help="skip the KV-cache decode measurement")
+    p.add_argument("--decode-only", action="store_true",
+                   help="run only the KV-cache decode measurement and print its JSON object (for rocprofv3)")
     p.add_argument("--rounds", type=int, default=1, help="headline: median ms over this many timed rounds of --steps")
     p.add_argument("--batch", type=int, default=0,
                    help="run the headline with this batch instead of the shape's (the line then says so)")
@@ -116,7 +118,7 @@ def log(*a):
 
 
 # Kernel symbol substring of each LaunchRecorder name (for counter CSVs).
-KERNEL_SYMBOLS = (("fused_forward_d128", "fused_stack_kernel"), ("attention", "attn_kernel"),
+KERNEL_SYMBOLS = (("fused_forward_d128", "fused_stack"), ("attention", "attn_kernel"),
                   ("gemm_", "gemm_"), ("residual_layernorm", "ln_"), ("layernorm", "ln_"))
 CALIBRATION_BYTES = 1 << 30
 
@@ -323,6 +325,10 @@ def main() -> int:
         sample = f"{x_cpu.shape[0]} x {x_cpu.shape[1]} tokens per call, {calls} calls" + (
             f" (causal prefix {prefix} of S={config.seq_len})" if prefix else "")
         return {"value": tokens / elapsed, "unit": "tokens/s", "cores": threads, "kind": "port", "sample": sample}, acc
+
+    if args.decode_only:
+        print(json.dumps({"decode": decode_leg(pkg, kernels, device, time_steps)}), flush=True)
+        return 0
 
     results = {}
     order = [args.workload] + ([] if (args.no_per_config or args.profile_only) else [i for i in CONFIG_NAMES if i != args.workload])

@@ -528,7 +528,7 @@ struct Lds {
 // the permuted k order (cop, own k-steps only).
 template <int HD, int HALF, int QB>
 __device__ __forceinline__ void attend16(const half_t* k_lds, const half_t* vt_lds, const half8_t (&qop)[OK],
-                                         half8_t (&cop)[KS], const float4_t& diag_mask, int g, int r16) {
+                                         half8_t (&cop)[KS], int g, int r16) {
   constexpr int H = D / HD;
   constexpr int HH = H / 2;
   constexpr int HDB = HD < 16 ? 1 : HD / 16;
@@ -558,7 +558,11 @@ __device__ __forceinline__ void attend16(const half_t* k_lds, const half_t* vt_l
         const half8_t kf = *reinterpret_cast<const half8_t*>(k_lds + (16 * kb + r16) * LD + 32 * (ks0 + j) + 8 * g);
         acc = mfma16x16x32(kf, qh[j], acc);
       }
-      if (kb == QB) acc += diag_mask;  // -inf above the diagonal
+      if (kb == QB) {  // -inf above the diagonal: key 4g + i vs query r16, formed here so nothing stays live
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (4 * g + i > r16) acc[i] = -INFINITY;
+      }
       sc[kb] = acc;
       mx = fmaxf(mx, fmaxf(fmaxf(acc[0], acc[1]), fmaxf(acc[2], acc[3])));
     }
@@ -605,6 +609,11 @@ __device__ __forceinline__ void attend16(const half_t* k_lds, const half_t* vt_l
         for (int i = 0; i < 4; ++i) cop[c / 2][4 * (c & 1) + i] = v[i];
       }
     }
+    // Narrow heads: interleaving more than two of them only raises register
+    // pressure past the 128 VGPRs of four waves per SIMD (and spills).
+    if constexpr (HD <= 16) {
+      if (hh % 2 == 1) __builtin_amdgcn_sched_barrier(0);
+    }
   }
 }
 
@@ -630,12 +639,8 @@ __device__ __forceinline__ void stack16_body(Lds& L, const float* __restrict__ x
 
   const int lane = threadIdx.x % kWave;
   const int g = lane / 16, r16 = lane % 16;
-  float4_t diag_mask;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) diag_mask[i] = (4 * g + i > r16) ? -INFINITY : 0.f;
   const int64_t seq = blockIdx.x;
   const float* xs = x + seq * S * D;
-  float* ys = y + seq * S * D;
   const int groups = layers * MATS;
 
   auto issue_group = [&](int gi) {
@@ -731,14 +736,14 @@ __device__ __forceinline__ void stack16_body(Lds& L, const float* __restrict__ x
 #pragma unroll
     for (int j = 0; j < OK; ++j) cop[OK * half + j] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
     switch (tb) {
-      case 0: attend16<HD, HALF, 0>(k_lds, vt_lds, qop, cop, diag_mask, g, r16); break;
-      case 1: attend16<HD, HALF, 1>(k_lds, vt_lds, qop, cop, diag_mask, g, r16); break;
-      case 2: attend16<HD, HALF, 2>(k_lds, vt_lds, qop, cop, diag_mask, g, r16); break;
-      case 3: attend16<HD, HALF, 3>(k_lds, vt_lds, qop, cop, diag_mask, g, r16); break;
-      case 4: attend16<HD, HALF, 4>(k_lds, vt_lds, qop, cop, diag_mask, g, r16); break;
-      case 5: attend16<HD, HALF, 5>(k_lds, vt_lds, qop, cop, diag_mask, g, r16); break;
-      case 6: attend16<HD, HALF, 6>(k_lds, vt_lds, qop, cop, diag_mask, g, r16); break;
-      default: attend16<HD, HALF, 7>(k_lds, vt_lds, qop, cop, diag_mask, g, r16); break;
+      case 0: attend16<HD, HALF, 0>(k_lds, vt_lds, qop, cop, g, r16); break;
+      case 1: attend16<HD, HALF, 1>(k_lds, vt_lds, qop, cop, g, r16); break;
+      case 2: attend16<HD, HALF, 2>(k_lds, vt_lds, qop, cop, g, r16); break;
+      case 3: attend16<HD, HALF, 3>(k_lds, vt_lds, qop, cop, g, r16); break;
+      case 4: attend16<HD, HALF, 4>(k_lds, vt_lds, qop, cop, g, r16); break;
+      case 5: attend16<HD, HALF, 5>(k_lds, vt_lds, qop, cop, g, r16); break;
+      case 6: attend16<HD, HALF, 6>(k_lds, vt_lds, qop, cop, g, r16); break;
+      default: attend16<HD, HALF, 7>(k_lds, vt_lds, qop, cop, g, r16); break;
     }
     lds_barrier();  // every wave is done with K and V^T: their areas take exchanges now
     {
@@ -799,15 +804,22 @@ __device__ __forceinline__ void stack16_body(Lds& L, const float* __restrict__ x
   const float* bf = gf + D;
   float mean, rstd;
   split_row_stats(res, xstat[0], wave, lane, mean, rstd);
-  if (tok < S) {
+  // The output address is rebuilt from an opaque copy of the lane id, so the
+  // compiler does not keep the input-side token offset live across the layer
+  // loop (at 128 VGPRs it would spill it).
+  int lane_o = lane;
+  asm volatile("" : "+v"(lane_o));
+  const int tok_o = 16 * tb + lane_o % 16, g_o = lane_o / 16;
+  if (tok_o < S) {
+    float* yrow = y + (seq * S + tok_o) * D;
 #pragma unroll
     for (int j = 0; j < OB; ++j) {
-      const int f0 = 16 * (OB * half + j) + 4 * g;
+      const int f0 = 16 * (OB * half + j) + 4 * g_o;
       const float4_t gg = ld4(gf + f0), bb = ld4(bf + f0);
       float4_t o;
 #pragma unroll
       for (int i = 0; i < 4; ++i) o[i] = (res[j][i] - mean) * rstd * gg[i] + bb[i];
-      *reinterpret_cast<float4_t*>(ys + (int64_t)tok * D + f0) = o;
+      *reinterpret_cast<float4_t*>(yrow + f0) = o;
     }
   }
 }
