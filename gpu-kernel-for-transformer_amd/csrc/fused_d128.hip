@@ -463,9 +463,14 @@ __device__ __forceinline__ void split_row_stats(const float4_t (&r)[OB], float2*
 #pragma unroll
     for (int i = 0; i < 4; ++i) { const float c = r[j][i] - ma; q += c * c; }
   const float m2a = quad_group_sum(q);
-  if (lane < 16) xs[wave * 16 + lane] = make_float2(ma, m2a);
+  // Addresses from an opaque copy of the lane id: rebuilt here each time
+  // rather than kept live (and spilled, whose reload would wait on vmcnt(0),
+  // i.e. on the weight DMA in flight).
+  int l = lane;
+  asm volatile("" : "+v"(l));
+  if (l < 16) xs[wave * 16 + l] = make_float2(ma, m2a);
   lds_barrier();
-  const float2 pb = xs[(wave ^ 8) * 16 + lane % 16];
+  const float2 pb = xs[(wave ^ 8) * 16 + l % 16];
   const float d = pb.x - ma;
   mean = 0.5f * (ma + pb.x);
   rstd = __builtin_amdgcn_rsqf(((m2a + pb.y) + d * d * 32.f) * (1.0f / D) + 1e-5f);
