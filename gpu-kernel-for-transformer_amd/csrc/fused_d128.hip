@@ -533,7 +533,12 @@ struct Lds {
 // the permuted k order (cop, own k-steps only).
 template <int HD, int HALF, int QB>
 __device__ __forceinline__ void attend16(const half_t* k_lds, const half_t* vt_lds, const half8_t (&qop)[OK],
-                                         half8_t (&cop)[KS], int g, int r16) {
+                                         half8_t (&cop)[KS], int g_in, int r16_in) {
+  // Opaque copies: the lane-dependent head masks and addresses below are then
+  // rebuilt in each call instead of being hoisted out of the layer loop and
+  // spilled.
+  int g = g_in, r16 = r16_in;
+  asm volatile("" : "+v"(g), "+v"(r16));
   constexpr int H = D / HD;
   constexpr int HH = H / 2;
   constexpr int HDB = HD < 16 ? 1 : HD / 16;
