@@ -477,24 +477,40 @@ __device__ __forceinline__ void split_row_stats(const float4_t (&r)[OB], float2*
 }
 
 // LayerNorm of the wave's half of the block -> its two k-steps of operand.
+// affine (wave-uniform): apply gamma / beta; the host clears it when they are
+// exactly 1 and 0 (the reference skips them then too, TTB:568-596), which
+// changes no bit of the result.
 __device__ __forceinline__ void split_layer_norm(const float4_t (&res)[OB], const float* gamma, const float* beta,
-                                                 float2* xs, int wave, int lane, int half, int g,
+                                                 bool affine, float2* xs, int wave, int lane, int half, int g,
                                                  half8_t (&own)[OK]) {
   float mean, rstd;
   split_row_stats(res, xs, wave, lane, mean, rstd);
   const float shift = -mean * rstd;
+  if (affine) {
 #pragma unroll
-  for (int j = 0; j < OK; ++j) {
-    const int ks = OK * half + j;
-    float4_t lo, hi;
-    const float4_t g0 = ld4(gamma + 32 * ks + 4 * g), g1 = ld4(gamma + 32 * ks + 16 + 4 * g);
-    const float4_t b0 = ld4(beta + 32 * ks + 4 * g), b1 = ld4(beta + 32 * ks + 16 + 4 * g);
+    for (int j = 0; j < OK; ++j) {
+      const int ks = OK * half + j;
+      float4_t lo, hi;
+      const float4_t g0 = ld4(gamma + 32 * ks + 4 * g), g1 = ld4(gamma + 32 * ks + 16 + 4 * g);
+      const float4_t b0 = ld4(beta + 32 * ks + 4 * g), b1 = ld4(beta + 32 * ks + 16 + 4 * g);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      lo[i] = fmaf(fmaf(res[2 * j][i], rstd, shift), g0[i], b0[i]);
-      hi[i] = fmaf(fmaf(res[2 * j + 1][i], rstd, shift), g1[i], b1[i]);
+      for (int i = 0; i < 4; ++i) {
+        lo[i] = fmaf(fmaf(res[2 * j][i], rstd, shift), g0[i], b0[i]);
+        hi[i] = fmaf(fmaf(res[2 * j + 1][i], rstd, shift), g1[i], b1[i]);
+      }
+      own[j] = to_operand(lo, hi);
     }
-    own[j] = to_operand(lo, hi);
+  } else {
+#pragma unroll
+    for (int j = 0; j < OK; ++j) {
+      float4_t lo, hi;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        lo[i] = fmaf(res[2 * j][i], rstd, shift);
+        hi[i] = fmaf(res[2 * j + 1][i], rstd, shift);
+      }
+      own[j] = to_operand(lo, hi);
+    }
   }
 }
 
@@ -632,7 +648,7 @@ __device__ __forceinline__ void attend16(const half_t* k_lds, const half_t* vt_l
 template <int HD, int HALF>
 __device__ __forceinline__ void stack16_body(Lds& L, const float* __restrict__ x, float* __restrict__ y,
                                              const half_t* __restrict__ wpack, const float* __restrict__ ppack,
-                                             int S, int layers, int wave, int tb) {
+                                             int S, int layers, int64_t affine_mask, int wave, int tb) {
   constexpr int H = D / HD;
   static_assert(H >= 2, "heads split between the two halves");
   constexpr int HH = H / 2;                    // heads per half
@@ -692,7 +708,8 @@ __device__ __forceinline__ void stack16_body(Lds& L, const float* __restrict__ x
     half8_t xn[KS];
     {
       half8_t own[OK];
-      split_layer_norm(res, pp + P_G1, pp + P_BE1, xstat[0], wave, lane, half, g, own);
+      split_layer_norm(res, pp + P_G1, pp + P_BE1, (affine_mask >> min(2 * layer, 63)) & 1, xstat[0], wave, lane, half, g,
+                       own);
       put_half(area_a, own, xn, tb, half, lane);
     }
 
@@ -778,7 +795,8 @@ __device__ __forceinline__ void stack16_body(Lds& L, const float* __restrict__ x
     // ---- LN2, FFN -------------------------------------------------------------
     {
       half8_t own[OK];
-      split_layer_norm(res, pp + P_G2, pp + P_BE2, xstat[1], wave, lane, half, g, own);
+      split_layer_norm(res, pp + P_G2, pp + P_BE2, (affine_mask >> min(2 * layer + 1, 63)) & 1, xstat[1], wave, lane, half,
+                       g, own);
       put_half(area_a, own, xn, tb, half, lane);
     }
     half8_t hf[KS];
@@ -829,7 +847,7 @@ __device__ __forceinline__ void stack16_body(Lds& L, const float* __restrict__ x
       float4_t o;
 #pragma unroll
       for (int i = 0; i < 4; ++i) o[i] = (res[j][i] - mean) * rstd * gg[i] + bb[i];
-      *reinterpret_cast<float4_t*>(yrow + f0) = o;
+      *reinterpret_cast<float4_t*>(yrow + f0) = o;  // (final LN: always affine, once per token)
     }
   }
 }
@@ -837,15 +855,15 @@ __device__ __forceinline__ void stack16_body(Lds& L, const float* __restrict__ x
 template <int HD>
 __global__ __launch_bounds__(64 * NW, 1) void fused_stack16_kernel(
     const float* __restrict__ x, float* __restrict__ y, const half_t* __restrict__ wpack,
-    const float* __restrict__ ppack, int S, int layers) {
+    const float* __restrict__ ppack, int S, int layers, int64_t affine_mask) {
   __shared__ Lds lds;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int wi = wave % 8;
   const int tb = wi < 4 ? wi : 11 - wi;  // the four waves of a SIMD hold blocks b, 7-b (both halves)
   if (wave < 8)
-    stack16_body<HD, 0>(lds, x, y, wpack, ppack, S, layers, wave, tb);
+    stack16_body<HD, 0>(lds, x, y, wpack, ppack, S, layers, affine_mask, wave, tb);
   else
-    stack16_body<HD, 1>(lds, x, y, wpack, ppack, S, layers, wave, tb);
+    stack16_body<HD, 1>(lds, x, y, wpack, ppack, S, layers, affine_mask, wave, tb);
 }
 
 }  // namespace w16
@@ -875,10 +893,10 @@ __global__ void pack_fragments_kernel(const float* __restrict__ w, half_t* __res
 
 template <int HD>
 static hipError_t launch(const float* x, float* y, const half_t* w, const float* p, int64_t batch, int S,
-                         int layers, hipStream_t s) {
+                         int layers, int64_t affine_mask, hipStream_t s) {
   if constexpr (HD <= 64) {
     hipLaunchKernelGGL((w16::fused_stack16_kernel<HD>), dim3((unsigned)batch), dim3(64 * w16::NW), 0, s, x, y, w, p,
-                       S, layers);
+                       S, layers, affine_mask);
   } else {
     hipLaunchKernelGGL((fused_stack_kernel<HD>), dim3((unsigned)batch), dim3(64 * NW), 0, s, x, y, w, p, S, layers);
   }
@@ -906,13 +924,14 @@ extern "C" int xb_pack_linear_fragments(const float* w, void* out, int32_t n, in
 
 extern "C" int xb_fused_forward_d128(const float* x, float* y, const void* wpack, const float* ppack,
                                      int64_t batch, int32_t seq_len, int32_t heads, int32_t ffn_dim,
-                                     int32_t layers, void* stream) {
+                                     int32_t layers, int64_t affine_mask, void* stream) {
   if (batch < 0 || seq_len <= 0 || heads <= 0 || ffn_dim <= 0 || layers <= 0) return XB_ERR_BAD_SIZE;
   if (batch > 0x7fffffffLL) return XB_ERR_BAD_SIZE;
   if (seq_len > fused::SMAX || fused::D % heads != 0) return XB_ERR_UNSUPPORTED_SHAPE;
   const int hd = fused::D / heads;
   if (hd != 8 && hd != 16 && hd != 32 && hd != 64 && hd != 128) return XB_ERR_UNSUPPORTED_SHAPE;
   if (ffn_dim != 128) return XB_ERR_UNSUPPORTED_SHAPE;
+  if (layers > 31) affine_mask = -1;  // bits beyond the mask: always affine
   if (batch == 0) return XB_OK;
   if (!x || !y || !wpack || !ppack) return XB_ERR_NULL_POINTER;
   if (((uintptr_t)x | (uintptr_t)y | (uintptr_t)wpack | (uintptr_t)ppack) & 15u) return XB_ERR_MISALIGNED;
@@ -920,11 +939,11 @@ extern "C" int xb_fused_forward_d128(const float* x, float* y, const void* wpack
   const half_t* w = static_cast<const half_t*>(wpack);
   hipError_t e;
   switch (hd) {
-    case 8: e = fused::launch<8>(x, y, w, ppack, batch, seq_len, layers, s); break;
-    case 16: e = fused::launch<16>(x, y, w, ppack, batch, seq_len, layers, s); break;
-    case 32: e = fused::launch<32>(x, y, w, ppack, batch, seq_len, layers, s); break;
-    case 64: e = fused::launch<64>(x, y, w, ppack, batch, seq_len, layers, s); break;
-    default: e = fused::launch<128>(x, y, w, ppack, batch, seq_len, layers, s); break;
+    case 8: e = fused::launch<8>(x, y, w, ppack, batch, seq_len, layers, affine_mask, s); break;
+    case 16: e = fused::launch<16>(x, y, w, ppack, batch, seq_len, layers, affine_mask, s); break;
+    case 32: e = fused::launch<32>(x, y, w, ppack, batch, seq_len, layers, affine_mask, s); break;
+    case 64: e = fused::launch<64>(x, y, w, ppack, batch, seq_len, layers, affine_mask, s); break;
+    default: e = fused::launch<128>(x, y, w, ppack, batch, seq_len, layers, affine_mask, s); break;
   }
   return (int)e;
 }

@@ -417,11 +417,13 @@ def fused_forward_d128(
     ffn_dim: int,
     num_layers: int,
     out: Optional[torch.Tensor] = None,
+    affine_mask: int = -1,
 ) -> torch.Tensor:
     """Whole-stack forward for d_model 128 / seq_len <= 128 (see xb_fused_forward_d128).
 
     wpack / ppack come from UserOptimizedTransformer._fused_stack_parameters
-    (Wq and bq pre-multiplied by head_dim**-0.5 * log2(e)).
+    (Wq and bq pre-multiplied by head_dim**-0.5 * log2(e)).  affine_mask bit
+    2l / 2l+1 set = apply layer l's norm1 / norm2 gamma and beta (-1: all).
     """
     _require_device(x, "fused_forward_d128")
     if x.ndim != 3 or x.shape[-1] != 128 or x.dtype != torch.float32 or not x.is_contiguous():
@@ -432,7 +434,7 @@ def fused_forward_d128(
     check(
         _launch("fused_forward_d128", lambda: lib().xb_fused_forward_d128(
             x.data_ptr(), out.data_ptr(), wpack.data_ptr(), ppack.data_ptr(), batch, seq_len,
-            num_heads, ffn_dim, num_layers, stream_handle(x.device))),
+            num_heads, ffn_dim, num_layers, int(affine_mask), stream_handle(x.device))),
         "xb_fused_forward_d128",
     )
     return out

@@ -234,13 +234,13 @@ class UserOptimizedTransformer(nn.Module):
             and all(n.eps == 1e-5 and n.weight is not None and n.bias is not None for n in norms)
         )
 
-    def _fused_stack_parameters(self) -> Tuple[torch.Tensor, torch.Tensor]:
-        """Fragment-packed FP16 weights and FP32 bias/LayerNorm buffer, cached by version."""
+    def _fused_stack_parameters(self) -> Tuple[torch.Tensor, torch.Tensor, int]:
+        """Fragment-packed FP16 weights, FP32 bias/LayerNorm buffer and LayerNorm affine mask, cached by version."""
         params = list(self.parameters())
         key = tuple((p.data_ptr(), _tensor_version(p), p.device) for p in params)
         cached = self.__dict__.get("_fused_stack_cache")
         if cached is not None and cached[0] == key and all(k[1] is not None for k in key):
-            return cached[1], cached[2]
+            return cached[1], cached[2], cached[3]
         weights, vectors = [], []
         with torch.no_grad():
             for layer in self.layers:
@@ -258,8 +258,17 @@ class UserOptimizedTransformer(nn.Module):
             vectors += [self.final_norm.weight.detach().float(), self.final_norm.bias.detach().float()]
             wpack = torch.cat(weights).contiguous()
             ppack = torch.cat(vectors).contiguous()
-        self.__dict__["_fused_stack_cache"] = (key, wpack, ppack)
-        return wpack, ppack
+        affine_mask = self._fused_affine_mask()
+        self.__dict__["_fused_stack_cache"] = (key, wpack, ppack, affine_mask)
+        return wpack, ppack, affine_mask
+
+    def _fused_affine_mask(self) -> int:
+        """Bit 2l / 2l+1: layer l's norm1 / norm2 has a non-identity affine (see xb_fused_forward_d128)."""
+        mask = 0
+        for index, layer in enumerate(self.layers[:31]):
+            mask |= int(self._layer_norm_uses_affine(layer.norm1)) << (2 * index)
+            mask |= int(self._layer_norm_uses_affine(layer.norm2)) << (2 * index + 1)
+        return mask if len(self.layers) <= 31 else -1
 
     @staticmethod
     def _layer_norm_uses_affine(layer_norm: nn.LayerNorm) -> bool:
@@ -344,8 +353,9 @@ class UserOptimizedTransformer(nn.Module):
         """
         cfg = self.config
         if token_valid is None and cfg.causal and self._uses_fused_stack(x):
-            wpack, ppack = self._fused_stack_parameters()
-            return kernels.fused_forward_d128(x, wpack, ppack, cfg.num_heads, cfg.ffn_dim, len(self.layers), out=out)
+            wpack, ppack, affine_mask = self._fused_stack_parameters()
+            return kernels.fused_forward_d128(x, wpack, ppack, cfg.num_heads, cfg.ffn_dim, len(self.layers), out=out,
+                                              affine_mask=affine_mask)
 
         def attend(index: int, layer: TransformerBlockParameters, qkv: torch.Tensor) -> torch.Tensor:
             return kernels.attention(qkv, cfg.num_heads, key_valid=token_valid, causal=cfg.causal,

@@ -189,13 +189,18 @@ int xb_pack_linear_fragments(const float* w, void* out, int32_t n, int32_t k,
  *          b1 [ffn], b2 [128], norm1 gamma, beta, norm2 gamma, beta [128
  *          each]; then final_norm gamma, beta.
  * (softmax_scale is head_dim ** -0.5, torch_transformer_benchmark.py:215.)
+ *   affine_mask: bit 2l set = apply norm1 gamma/beta of layer l, bit 2l+1 =
+ *          norm2's; a clear bit skips an identity affine (gamma == 1,
+ *          beta == 0 exactly), as the reference does (TTB:568-596).  Pass -1
+ *          to always apply; layers beyond 31 always apply; the final norm
+ *          always applies.
  * Replaces _forward_cuda_fused_norm (torch_transformer_benchmark.py:1092-1148)
  * for the official d_model = 128 shapes.
  */
 int xb_fused_forward_d128(const float* x, float* y, const void* wpack,
                           const float* ppack, int64_t batch, int32_t seq_len,
                           int32_t heads, int32_t ffn_dim, int32_t layers,
-                          void* stream);
+                          int64_t affine_mask, void* stream);
 
 #ifdef __cplusplus
 }
