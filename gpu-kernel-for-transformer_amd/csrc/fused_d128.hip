@@ -9,7 +9,11 @@
 //   ... ; y = LN_final(x)
 // with FP16 MFMA operands, FP32 accumulation, FP32 residual and softmax.
 //
-// Layout.  Eight waves (two per SIMD) each own one 16-token block: wave w
+// Two kernels: fused_stack_kernel below (eight waves, used for head_dim 128)
+// and the sixteen-wave fused_stack16_kernel further down (head_dim <= 64),
+// which splits each token block's output features between two waves.
+//
+// Layout (eight-wave kernel).  Eight waves (two per SIMD) each own one 16-token block: wave w
 // holds block w for w < 4 and block 11-w otherwise, so the two waves sharing
 // a SIMD (w and w+4) hold blocks b and 7-b and every SIMD gets the same causal
 // attention work.  The residual stream stays in registers in the C layout of
