@@ -79,7 +79,7 @@ _SIGNATURES = {
         [_vp, _vp, _vp, _vp, _i32, _i64, _i32, _i32, _i64, _i64, _f32, _vp, _i64, _vp],
     ),
     "xb_pack_linear_fragments": (ctypes.c_int, [_vp, _vp, _i32, _i32, _i32, _f32, _vp]),
-    "xb_fused_forward_d128": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i64, _vp]),
+    "xb_fused_forward_d128": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i64, _vp, _i32, _vp]),
 }
 
 _LIB: Optional[ctypes.CDLL] = None

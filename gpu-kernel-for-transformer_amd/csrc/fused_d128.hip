@@ -542,6 +542,7 @@ struct Lds {
   __attribute__((aligned(1024))) char wst[2][MAT_BYTES];  // weight matrix stages
   float prm[2][P_LAYER];                               // per-layer vectors, by layer parity
   float2 xstat[2][NW * 16];                            // LayerNorm partial statistics
+  uint8_t kval[SMAX];                                  // MASKED: token t may be attended to / is output
 };
 
 // Causal attention of query block QB (keys 0 .. 16 QB + 15) for the heads of
@@ -551,9 +552,13 @@ struct Lds {
 // query fit in registers, so the softmax needs no running rescale; row sums
 // come from an all-ones A operand.  The context leaves as MFMA operands in
 // the permuted k order (cop, own k-steps only).
-template <int HD, int HALF, int QB>
-__device__ __forceinline__ void attend16(const half_t* k_lds, const half_t* vt_lds, const half8_t (&qop)[OK],
-                                         half8_t (&cop)[KS], int g_in, int r16_in) {
+// MODE 0: causal, every key valid.  MODE 1: causal plus the key validity
+// bytes kval (padding, and tokens past S).  MODE 2: no causal mask, key
+// validity only (every query block sees all eight key blocks).  In modes 1
+// and 2 a query may see no key at all: it then gets a zero context.
+template <int HD, int HALF, int QB, int MODE>
+__device__ __forceinline__ void attend16(const half_t* k_lds, const half_t* vt_lds, const uint8_t* kval,
+                                         const half8_t (&qop)[OK], half8_t (&cop)[KS], int g_in, int r16_in) {
   // Opaque copies: the lane-dependent head masks and addresses below are then
   // rebuilt in each call instead of being hoisted out of the layer loop and
   // spilled.
@@ -563,7 +568,8 @@ __device__ __forceinline__ void attend16(const half_t* k_lds, const half_t* vt_l
   constexpr int HH = H / 2;
   constexpr int HDB = HD < 16 ? 1 : HD / 16;
   constexpr int KSH = HD >= 32 ? HD / 32 : 1;
-  constexpr int NKT = QB / 2 + 1;  // 32-key steps of the PV product
+  constexpr int LKB = MODE == 2 ? 7 : QB;  // last key block
+  constexpr int NKT = LKB / 2 + 1;          // 32-key steps of the PV product
 #pragma unroll
   for (int hh = 0; hh < HH; ++hh) {
     const int h = HH * HALF + hh;
@@ -578,25 +584,32 @@ __device__ __forceinline__ void attend16(const half_t* k_lds, const half_t* vt_l
           if ((32 * ks0 + 4 * g + (m & 3) + 16 * (m >> 2)) / HD != h) qh[j][m] = (half_t)0.f;
       }
     }
-    float4_t sc[QB + 1];
+    float4_t sc[LKB + 1];
     float mx = -INFINITY;
 #pragma unroll
-    for (int kb = 0; kb <= QB; ++kb) {
+    for (int kb = 0; kb <= LKB; ++kb) {
       float4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int j = 0; j < KSH; ++j) {
         const half8_t kf = *reinterpret_cast<const half8_t*>(k_lds + (16 * kb + r16) * LD + 32 * (ks0 + j) + 8 * g);
         acc = mfma16x16x32(kf, qh[j], acc);
       }
-      if (kb == QB) {  // -inf above the diagonal: key 4g + i vs query r16, formed here so nothing stays live
+      if (MODE != 2 && kb == QB) {  // -inf above the diagonal: key 4g + i vs query r16, formed here so nothing stays live
 #pragma unroll
         for (int i = 0; i < 4; ++i)
           if (4 * g + i > r16) acc[i] = -INFINITY;
+      }
+      if constexpr (MODE != 0) {  // keys 16 kb + 4g .. +3: validity bytes
+        const uint32_t v4 = *reinterpret_cast<const uint32_t*>(kval + 16 * kb + 4 * g);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (((v4 >> (8 * i)) & 0xffu) == 0u) acc[i] = -INFINITY;
       }
       sc[kb] = acc;
       mx = fmaxf(mx, fmaxf(fmaxf(acc[0], acc[1]), fmaxf(acc[2], acc[3])));
     }
     mx = quad_group_max(mx);
+    if constexpr (MODE != 0) mx = mx == -INFINITY ? 0.f : mx;  // no visible key: every p is exp2(-inf) = 0
     const half8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
     float4_t lacc = {0.f, 0.f, 0.f, 0.f};
     const int vrow0 = HD < 16 ? 16 * (h / 2) : h * HD;
@@ -608,7 +621,7 @@ __device__ __forceinline__ void attend16(const half_t* k_lds, const half_t* vt_l
       float4_t p0, p1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int i = 0; i < 4; ++i) p0[i] = __builtin_amdgcn_exp2f(sc[2 * kt][i] - mx);
-      if (2 * kt + 1 <= QB) {  // constant once the loop is unrolled
+      if (2 * kt + 1 <= LKB) {  // constant once the loop is unrolled
 #pragma unroll
         for (int i = 0; i < 4; ++i) p1[i] = __builtin_amdgcn_exp2f(sc[2 * kt + 1][i] - mx);
       }
@@ -621,7 +634,7 @@ __device__ __forceinline__ void attend16(const half_t* k_lds, const half_t* vt_l
         o[hb] = mfma16x16x32(vf, pf, o[hb]);
       }
     }
-    const float inv = __builtin_amdgcn_rcpf(lacc[0]);
+    const float inv = MODE == 0 || lacc[0] > 0.f ? __builtin_amdgcn_rcpf(lacc[0]) : 0.f;
     if constexpr (HD >= 16) {
 #pragma unroll
       for (int hb = 0; hb < HDB; ++hb) {
@@ -649,7 +662,9 @@ __device__ __forceinline__ void attend16(const half_t* k_lds, const half_t* vt_l
 
 // The kernel body for one half (HALF is a compile-time constant so that every
 // register-array index below is static).
-template <int HD, int HALF>
+// MASK: 0 causal with every token valid; 1 causal with key validity; 2 no
+// causal mask (validity marks tokens past S, and padding if given).
+template <int HD, int HALF, int MASK>
 __device__ __forceinline__ void stack16_body(Lds& L, const float* __restrict__ x, float* __restrict__ y,
                                              const half_t* __restrict__ wpack, const float* __restrict__ ppack,
                                              int S, int layers, int64_t affine_mask, int wave, int tb) {
@@ -767,14 +782,14 @@ __device__ __forceinline__ void stack16_body(Lds& L, const float* __restrict__ x
 #pragma unroll
     for (int j = 0; j < OK; ++j) cop[OK * half + j] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
     switch (tb) {
-      case 0: attend16<HD, HALF, 0>(k_lds, vt_lds, qop, cop, g, r16); break;
-      case 1: attend16<HD, HALF, 1>(k_lds, vt_lds, qop, cop, g, r16); break;
-      case 2: attend16<HD, HALF, 2>(k_lds, vt_lds, qop, cop, g, r16); break;
-      case 3: attend16<HD, HALF, 3>(k_lds, vt_lds, qop, cop, g, r16); break;
-      case 4: attend16<HD, HALF, 4>(k_lds, vt_lds, qop, cop, g, r16); break;
-      case 5: attend16<HD, HALF, 5>(k_lds, vt_lds, qop, cop, g, r16); break;
-      case 6: attend16<HD, HALF, 6>(k_lds, vt_lds, qop, cop, g, r16); break;
-      default: attend16<HD, HALF, 7>(k_lds, vt_lds, qop, cop, g, r16); break;
+      case 0: attend16<HD, HALF, 0, MASK>(k_lds, vt_lds, L.kval, qop, cop, g, r16); break;
+      case 1: attend16<HD, HALF, 1, MASK>(k_lds, vt_lds, L.kval, qop, cop, g, r16); break;
+      case 2: attend16<HD, HALF, 2, MASK>(k_lds, vt_lds, L.kval, qop, cop, g, r16); break;
+      case 3: attend16<HD, HALF, 3, MASK>(k_lds, vt_lds, L.kval, qop, cop, g, r16); break;
+      case 4: attend16<HD, HALF, 4, MASK>(k_lds, vt_lds, L.kval, qop, cop, g, r16); break;
+      case 5: attend16<HD, HALF, 5, MASK>(k_lds, vt_lds, L.kval, qop, cop, g, r16); break;
+      case 6: attend16<HD, HALF, 6, MASK>(k_lds, vt_lds, L.kval, qop, cop, g, r16); break;
+      default: attend16<HD, HALF, 7, MASK>(k_lds, vt_lds, L.kval, qop, cop, g, r16); break;
     }
     lds_barrier();  // every wave is done with K and V^T: their areas take exchanges now
     {
@@ -844,30 +859,40 @@ __device__ __forceinline__ void stack16_body(Lds& L, const float* __restrict__ x
   const int tok_o = 16 * tb + lane_o % 16, g_o = lane_o / 16;
   if (tok_o < S) {
     float* yrow = y + (seq * S + tok_o) * D;
+    // Padded tokens leave as zero rows (torch_transformer_benchmark.py:1146-1147).
+    const bool zero = MASK != 0 && L.kval[tok_o] == 0;
 #pragma unroll
     for (int j = 0; j < OB; ++j) {
       const int f0 = 16 * (OB * half + j) + 4 * g_o;
       const float4_t gg = ld4(gf + f0), bb = ld4(bf + f0);
       float4_t o;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = (res[j][i] - mean) * rstd * gg[i] + bb[i];
+      for (int i = 0; i < 4; ++i) o[i] = zero ? 0.f : (res[j][i] - mean) * rstd * gg[i] + bb[i];
       *reinterpret_cast<float4_t*>(yrow + f0) = o;  // (final LN: always affine, once per token)
     }
   }
 }
 
-template <int HD>
+template <int HD, int MASK>
 __global__ __launch_bounds__(64 * NW, 1) void fused_stack16_kernel(
     const float* __restrict__ x, float* __restrict__ y, const half_t* __restrict__ wpack,
-    const float* __restrict__ ppack, int S, int layers, int64_t affine_mask) {
+    const float* __restrict__ ppack, int S, int layers, int64_t affine_mask,
+    const uint8_t* __restrict__ token_valid) {
   __shared__ Lds lds;
+  if constexpr (MASK != 0) {
+    // Token t is valid iff t < S and its byte of token_valid ([B, S], NULL =
+    // all) is nonzero.  Visible after the first barrier in the body.
+    const int t = threadIdx.x;
+    if (t < SMAX)
+      lds.kval[t] = t < S && (token_valid == nullptr || token_valid[(int64_t)blockIdx.x * S + t] != 0) ? 1 : 0;
+  }
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int wi = wave % 8;
   const int tb = wi < 4 ? wi : 11 - wi;  // the four waves of a SIMD hold blocks b, 7-b (both halves)
   if (wave < 8)
-    stack16_body<HD, 0>(lds, x, y, wpack, ppack, S, layers, affine_mask, wave, tb);
+    stack16_body<HD, 0, MASK>(lds, x, y, wpack, ppack, S, layers, affine_mask, wave, tb);
   else
-    stack16_body<HD, 1>(lds, x, y, wpack, ppack, S, layers, affine_mask, wave, tb);
+    stack16_body<HD, 1, MASK>(lds, x, y, wpack, ppack, S, layers, affine_mask, wave, tb);
 }
 
 }  // namespace w16
@@ -897,10 +922,18 @@ __global__ void pack_fragments_kernel(const float* __restrict__ w, half_t* __res
 
 template <int HD>
 static hipError_t launch(const float* x, float* y, const half_t* w, const float* p, int64_t batch, int S,
-                         int layers, int64_t affine_mask, hipStream_t s) {
+                         int layers, int64_t affine_mask, const uint8_t* token_valid, int causal, hipStream_t s) {
   if constexpr (HD <= 64) {
-    hipLaunchKernelGGL((w16::fused_stack16_kernel<HD>), dim3((unsigned)batch), dim3(64 * w16::NW), 0, s, x, y, w, p,
-                       S, layers, affine_mask);
+    const dim3 grid((unsigned)batch), block(64 * w16::NW);
+    if (!causal)
+      hipLaunchKernelGGL((w16::fused_stack16_kernel<HD, 2>), grid, block, 0, s, x, y, w, p, S, layers, affine_mask,
+                         token_valid);
+    else if (token_valid != nullptr)
+      hipLaunchKernelGGL((w16::fused_stack16_kernel<HD, 1>), grid, block, 0, s, x, y, w, p, S, layers, affine_mask,
+                         token_valid);
+    else
+      hipLaunchKernelGGL((w16::fused_stack16_kernel<HD, 0>), grid, block, 0, s, x, y, w, p, S, layers, affine_mask,
+                         token_valid);
   } else {
     hipLaunchKernelGGL((fused_stack_kernel<HD>), dim3((unsigned)batch), dim3(64 * NW), 0, s, x, y, w, p, S, layers);
   }
@@ -928,12 +961,14 @@ extern "C" int xb_pack_linear_fragments(const float* w, void* out, int32_t n, in
 
 extern "C" int xb_fused_forward_d128(const float* x, float* y, const void* wpack, const float* ppack,
                                      int64_t batch, int32_t seq_len, int32_t heads, int32_t ffn_dim,
-                                     int32_t layers, int64_t affine_mask, void* stream) {
+                                     int32_t layers, int64_t affine_mask, const uint8_t* token_valid,
+                                     int32_t causal, void* stream) {
   if (batch < 0 || seq_len <= 0 || heads <= 0 || ffn_dim <= 0 || layers <= 0) return XB_ERR_BAD_SIZE;
   if (batch > 0x7fffffffLL) return XB_ERR_BAD_SIZE;
   if (seq_len > fused::SMAX || fused::D % heads != 0) return XB_ERR_UNSUPPORTED_SHAPE;
   const int hd = fused::D / heads;
   if (hd != 8 && hd != 16 && hd != 32 && hd != 64 && hd != 128) return XB_ERR_UNSUPPORTED_SHAPE;
+  if (hd == 128 && (token_valid != nullptr || !causal)) return XB_ERR_UNSUPPORTED_SHAPE;  // eight-wave kernel: causal only
   if (ffn_dim != 128) return XB_ERR_UNSUPPORTED_SHAPE;
   if (layers > 31) affine_mask = -1;  // bits beyond the mask: always affine
   if (batch == 0) return XB_OK;
@@ -943,11 +978,11 @@ extern "C" int xb_fused_forward_d128(const float* x, float* y, const void* wpack
   const half_t* w = static_cast<const half_t*>(wpack);
   hipError_t e;
   switch (hd) {
-    case 8: e = fused::launch<8>(x, y, w, ppack, batch, seq_len, layers, affine_mask, s); break;
-    case 16: e = fused::launch<16>(x, y, w, ppack, batch, seq_len, layers, affine_mask, s); break;
-    case 32: e = fused::launch<32>(x, y, w, ppack, batch, seq_len, layers, affine_mask, s); break;
-    case 64: e = fused::launch<64>(x, y, w, ppack, batch, seq_len, layers, affine_mask, s); break;
-    default: e = fused::launch<128>(x, y, w, ppack, batch, seq_len, layers, affine_mask, s); break;
+    case 8: e = fused::launch<8>(x, y, w, ppack, batch, seq_len, layers, affine_mask, token_valid, causal, s); break;
+    case 16: e = fused::launch<16>(x, y, w, ppack, batch, seq_len, layers, affine_mask, token_valid, causal, s); break;
+    case 32: e = fused::launch<32>(x, y, w, ppack, batch, seq_len, layers, affine_mask, token_valid, causal, s); break;
+    case 64: e = fused::launch<64>(x, y, w, ppack, batch, seq_len, layers, affine_mask, token_valid, causal, s); break;
+    default: e = fused::launch<128>(x, y, w, ppack, batch, seq_len, layers, affine_mask, token_valid, causal, s); break;
   }
   return (int)e;
 }

@@ -418,12 +418,16 @@ def fused_forward_d128(
     num_layers: int,
     out: Optional[torch.Tensor] = None,
     affine_mask: int = -1,
+    token_valid: Optional[torch.Tensor] = None,
+    causal: bool = True,
 ) -> torch.Tensor:
     """Whole-stack forward for d_model 128 / seq_len <= 128 (see xb_fused_forward_d128).
 
     wpack / ppack come from UserOptimizedTransformer._fused_stack_parameters
     (Wq and bq pre-multiplied by head_dim**-0.5 * log2(e)).  affine_mask bit
     2l / 2l+1 set = apply layer l's norm1 / norm2 gamma and beta (-1: all).
+    token_valid ([B, S] bool/uint8) and causal=False give the padding and
+    non-causal semantics of `attention` (padded rows come out zero).
     """
     _require_device(x, "fused_forward_d128")
     if x.ndim != 3 or x.shape[-1] != 128 or x.dtype != torch.float32 or not x.is_contiguous():
@@ -431,10 +435,12 @@ def fused_forward_d128(
     batch, seq_len, _ = x.shape
     if out is None:
         out = torch.empty_like(x)
+    valid = None if token_valid is None else _byte_mask(token_valid, batch * seq_len, x.device, "token_valid")
     check(
         _launch("fused_forward_d128", lambda: lib().xb_fused_forward_d128(
             x.data_ptr(), out.data_ptr(), wpack.data_ptr(), ppack.data_ptr(), batch, seq_len,
-            num_heads, ffn_dim, num_layers, int(affine_mask), stream_handle(x.device))),
+            num_heads, ffn_dim, num_layers, int(affine_mask), _ptr(valid), int(bool(causal)),
+            stream_handle(x.device))),
         "xb_fused_forward_d128",
     )
     return out

@@ -352,10 +352,11 @@ class UserOptimizedTransformer(nn.Module):
         with at least one zero.
         """
         cfg = self.config
-        if token_valid is None and cfg.causal and self._uses_fused_stack(x):
+        masked = token_valid is not None or not cfg.causal
+        if self._uses_fused_stack(x) and (not masked or cfg.head_dim <= 64):
             wpack, ppack, affine_mask = self._fused_stack_parameters()
             return kernels.fused_forward_d128(x, wpack, ppack, cfg.num_heads, cfg.ffn_dim, len(self.layers), out=out,
-                                              affine_mask=affine_mask)
+                                              affine_mask=affine_mask, token_valid=token_valid, causal=cfg.causal)
 
         def attend(index: int, layer: TransformerBlockParameters, qkv: torch.Tensor) -> torch.Tensor:
             return kernels.attention(qkv, cfg.num_heads, key_valid=token_valid, causal=cfg.causal,

@@ -38,7 +38,7 @@ extern "C" {
 
 /* GEMM epilogues applied to (A . W^T + bias) before the FP16 store. */
 #define XB_EPI_BIAS 0       /* y = acc + bias                                  */
-#define XB_EPI_BIAS_GELU 1  /* y = gelu_erf(acc + bias) (exact erf, not tanh)  */
+#define XB_EPI_BIAS_GELU 1  /* y = gelu(acc + bias), erf form to 3e-5 (not tanh) */
 
 /* Row masks of xb_residual_layernorm_masked (bits; rows whose valid byte is 0). */
 #define XB_MASK_UPDATE 1    /* the update is dropped: s = residual             */
@@ -194,13 +194,19 @@ int xb_pack_linear_fragments(const float* w, void* out, int32_t n, int32_t k,
  *          beta == 0 exactly), as the reference does (TTB:568-596).  Pass -1
  *          to always apply; layers beyond 31 always apply; the final norm
  *          always applies.
+ *   token_valid ([batch, seq_len] bytes, NULL = all valid) and causal: the
+ *          padding and non-causal semantics of xb_attention (padded tokens
+ *          are masked as keys in every layer and leave as zero rows, a query
+ *          that sees no key gets a zero context).  head_dim 128 takes only
+ *          causal = 1 with token_valid = NULL.
  * Replaces _forward_cuda_fused_norm (torch_transformer_benchmark.py:1092-1148)
  * for the official d_model = 128 shapes.
  */
 int xb_fused_forward_d128(const float* x, float* y, const void* wpack,
                           const float* ppack, int64_t batch, int32_t seq_len,
                           int32_t heads, int32_t ffn_dim, int32_t layers,
-                          int64_t affine_mask, void* stream);
+                          int64_t affine_mask, const uint8_t* token_valid,
+                          int32_t causal, void* stream);
 
 #ifdef __cplusplus
 }
