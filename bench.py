@@ -360,9 +360,11 @@ def main() -> int:
                 run = lambda: model(x)  # noqa: E731  (launch-overhead-free at this size)
                 mode = "eager"
             else:
-                graphed = graphs.FixedInputCUDAGraph(model, x, None)
-                run = lambda: graphed(x)  # noqa: E731  (clone included, as the reference's replay)
-                mode = "hipGraph replay"
+                # The reference harness's choice (cuda_graph_runner.maybe_cuda_graph):
+                # replay with the output clone, or eager for a one-kernel forward.
+                runner, graphed, status = graphs.maybe_cuda_graph(model, x, None, enabled=True)
+                run = lambda: runner(x)  # noqa: E731
+                mode = "hipGraph replay" if graphed else f"eager: {status}"
             if big or (is_head and args.rounds == 1):
                 ms, wall = time_steps(run, steps, warmup)
             elif is_head:

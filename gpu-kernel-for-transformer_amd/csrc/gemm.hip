@@ -153,8 +153,11 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_nt_kernel(
 // Large-tile kernel for K % 64 == 0.  8 waves (2 per SIMD) share a BM x BN
 // tile; each wave owns a (BM/WGM) x (BN/WGN) sub-tile with its FP32
 // accumulators in VGPRs.  Operands reach LDS by direct global -> LDS loads
-// (global_load_lds_dwordx4), one 64-wide K slab at a time, double buffered:
-// slab kt+2 is requested as soon as every wave has read slab kt.
+// (global_load_lds_dwordx4), one 64-wide K slab at a time, in a ring of ST
+// slab stages: slab kt+ST is requested as soon as every wave has read slab
+// kt, so ST-1 slabs are in flight while one is consumed.  With one block per
+// CU nothing else hides the memory latency, so the ring depth is what keeps
+// the MFMAs fed when the grid is a single round of tiles.
 //
 // LDS slab layout: the A rows (BM) and then the W rows (BN), 128 bytes each
 // (64 halves = eight 16-byte chunks).  Chunk c of row r lives at slot
@@ -184,7 +187,7 @@ __device__ __forceinline__ void slab_barrier() {
 
 __device__ __forceinline__ int row128_offset(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
 
-template <int BM, int BN, int WGM, int WGN, int EPI>
+template <int BM, int BN, int WGM, int WGN, int EPI, int ST>
 __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_kernel(
     const half_t* __restrict__ A, const half_t* __restrict__ W,
     const float* __restrict__ bias, half_t* __restrict__ C, int M, int N,
@@ -195,7 +198,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_kernel(
   constexpr int SEGS = (BM + BN) / 8;          // 1 KB wave-loads per slab (8 rows)
   constexpr int SPW = SEGS / NW;
   static_assert(SEGS % NW == 0 && WM % 16 == 0 && WN % 16 == 0, "tile shape");
-  __shared__ __attribute__((aligned(1024))) char smem[2 * SLAB];
+  static_assert(ST >= 2 && ST * SLAB <= 160 * 1024 && (ST - 1) * SPW < 64, "slab ring");
+  __shared__ __attribute__((aligned(1024))) char smem[ST * SLAB];
   const int tile = xcd_contiguous_tile(blockIdx.x, gridDim.x);
   const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
   const int lane = threadIdx.x % kWave;
@@ -221,8 +225,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_kernel(
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
   const int KT = K / 64;
-  auto read_frags = [&](int kt, int ks, half8_t (&af)[FM], half8_t (&bf)[FN]) {
-    const char* st = smem + (kt & 1) * SLAB;
+  auto read_frags = [&](int stage, int ks, half8_t (&af)[FM], half8_t (&bf)[FN]) {
+    const char* st = smem + stage * SLAB;
     const int q = ks * 4 + lane / 16;
 #pragma unroll
     for (int j = 0; j < FN; ++j)
@@ -238,30 +242,36 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_kernel(
       for (int j = 0; j < FN; ++j) acc[i][j] = mfma16x16x32(bf[j], af[i], acc[i][j]);
   };
   // Slab kt: sub-step 0 reads sub-step 1's fragments of the same slab while
-  // its own MFMAs run; sub-step 1 waits for slab kt+1, refills slab kt's stage
-  // with slab kt+2 and reads slab kt+1's first fragments.
+  // its own MFMAs run; sub-step 1 waits for slab kt+1 (leaving the ST-2 slabs
+  // after it in flight), refills slab kt's stage with slab kt+ST and reads
+  // slab kt+1's first fragments.  vmcnt retires loads in issue order, so
+  // "at most (ST-2)*SPW outstanding" means slab kt+1 has landed.
   half8_t a0[FM], b0[FN], a1[FM], b1[FN];
-  issue(0, 0);
-  if (KT > 1) issue(1, 1);
-  if (KT > 1) wait_vm_lgkm0<SPW>(); else wait_vm_lgkm0<0>();
+#pragma unroll
+  for (int s = 0; s < ST; ++s)
+    if (s < KT) issue(s, s);
+  if (KT >= ST) wait_vm_lgkm0<(ST - 1) * SPW>(); else wait_vm_lgkm0<0>();
   slab_barrier();
   read_frags(0, 0, a0, b0);
+  int stage = 0;  // stage of slab kt
   for (int kt = 0; kt < KT; ++kt) {
+    const int next = stage + 1 == ST ? 0 : stage + 1;
     __builtin_amdgcn_sched_barrier(0);
-    read_frags(kt, 1, a1, b1);
+    read_frags(stage, 1, a1, b1);
     __builtin_amdgcn_sched_barrier(0);
     mma(a0, b0);
     __builtin_amdgcn_sched_barrier(0);
     if (kt + 1 < KT) {
-      wait_vm_lgkm0<0>();
+      if (kt + ST - 1 < KT) wait_vm_lgkm0<(ST - 2) * SPW>(); else wait_vm_lgkm0<0>();
       slab_barrier();
-      if (kt + 2 < KT) issue(kt + 2, kt & 1);
-      read_frags(kt + 1, 0, a0, b0);
+      if (kt + ST < KT) issue(kt + ST, stage);
+      read_frags(next, 0, a0, b0);
     } else {
       wait_vm_lgkm0<0>();
     }
     __builtin_amdgcn_sched_barrier(0);
     mma(a1, b1);
+    stage = next;
   }
 
   // Epilogue: lane owns C[m][n .. n+3] for each (i, j); bias (+ GELU) in FP32
@@ -291,12 +301,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_kernel(
   }
 }
 
-template <int BM, int BN, int WGM, int WGN, int EPI>
+template <int BM, int BN, int WGM, int WGN, int EPI, int ST>
 static hipError_t launch_gemm_dma(const half_t* a, const half_t* w, const float* bias, half_t* c,
                                   int64_t m, int n, int k, hipStream_t s) {
   const int64_t tm = (m + BM - 1) / BM, tn = (n + BN - 1) / BN;
   if (tm * tn > 0x7fffffffLL) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, WGM, WGN, EPI>), dim3((unsigned)(tm * tn)),
+  hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, WGM, WGN, EPI, ST>), dim3((unsigned)(tm * tn)),
                      dim3(64 * WGM * WGN), 0, s, a, w, bias, c, (int)m, n, k, (int)tn);
   return hipGetLastError();
 }
@@ -324,10 +334,10 @@ static hipError_t dispatch_gemm(const half_t* a, const half_t* w, const float* b
     const int64_t wide = n % 192 == 0 ? (tiles(256, 192) + 255) / 256 * 49152 * 90 / 100 : INT64_MAX;
     const int64_t mid = (tiles(128, 256) + 255) / 256 * 32768;
     const int64_t small = (tiles(128, 128) + 255) / 256 * 16384 * 115 / 100;
-    if (big <= wide && big <= mid && big <= small) return launch_gemm_dma<256, 256, 4, 2, EPI>(a, w, bias, c, m, n, k, s);
-    if (wide <= mid && wide <= small) return launch_gemm_dma<256, 192, 4, 2, EPI>(a, w, bias, c, m, n, k, s);
-    if (mid <= small) return launch_gemm_dma<128, 256, 2, 4, EPI>(a, w, bias, c, m, n, k, s);
-    return launch_gemm_dma<128, 128, 2, 2, EPI>(a, w, bias, c, m, n, k, s);
+    if (big <= wide && big <= mid && big <= small) return launch_gemm_dma<256, 256, 4, 2, EPI, 2>(a, w, bias, c, m, n, k, s);
+    if (wide <= mid && wide <= small) return launch_gemm_dma<256, 192, 4, 2, EPI, 2>(a, w, bias, c, m, n, k, s);
+    if (mid <= small) return launch_gemm_dma<128, 256, 2, 4, EPI, 2>(a, w, bias, c, m, n, k, s);
+    return launch_gemm_dma<128, 128, 2, 2, EPI, 2>(a, w, bias, c, m, n, k, s);
   }
   if (tiles(128, 128) >= 512) return launch_gemm<128, 128, 2, 2, EPI>(a, w, bias, c, m, n, k, s);
   return launch_gemm<64, 64, 2, 2, EPI>(a, w, bias, c, m, n, k, s);

@@ -8,7 +8,9 @@ kept for drop-in use; on ROCm `torch.cuda.CUDAGraph` captures a hipGraph):
     captured `_version`, otherwise run eagerly;
   - return a clone of the static output (callers get independent tensors);
   - `maybe_cuda_graph` validates one replay bitwise against eager and falls
-    back to eager on any capture error or mismatch.
+    back to eager on any capture error or mismatch.  A forward that is a
+    single kernel launch (the whole-stack d_model 128 kernel) is not
+    captured: its replay would be that one launch plus the output copy.
 The kernels issue no hipMemsetAsync and allocate nothing themselves, so a
 captured forward is a plain chain of kernel nodes.
 """
@@ -90,6 +92,9 @@ def maybe_cuda_graph(model: nn.Module, x: torch.Tensor, valid_token_mask: Option
         return model, True, str(getattr(model, "graph_status", "internal graph replay"))
     if bool(getattr(model, "_kv_cache_enabled", False)):
         return model, False, "stateful KV-cache decoding uses the eager path"
+    single_launch = getattr(model, "_single_launch_forward", None)
+    if single_launch is not None and single_launch(x, valid_token_mask):
+        return model, False, "one-kernel forward: launched eagerly (a replay adds only the output copy)"
     try:
         with torch.inference_mode():
             eager = model(x, valid_token_mask)

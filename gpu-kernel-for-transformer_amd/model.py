@@ -92,6 +92,24 @@ def _tensor_version(tensor: torch.Tensor) -> Optional[int]:
         return None
 
 
+# Generation of the process's module trees: torch calls these global hooks
+# whenever any nn.Module registers a parameter or a submodule by assignment,
+# so a model's cached walk of its own tree (parameter list, LayerNorms) is
+# redone only after some tree may have changed, not on every forward.  The
+# walk itself (Module.parameters / modules) costs tens of microseconds, as
+# much as a whole small forward.
+_TREE_GENERATION = [0]
+
+
+def _tree_changed(*_args) -> None:
+    _TREE_GENERATION[0] += 1
+    return None
+
+
+nn.modules.module.register_module_parameter_registration_hook(_tree_changed)
+nn.modules.module.register_module_module_registration_hook(_tree_changed)
+
+
 class _LayerWeights:
     """FP16 GEMM operands and FP32 biases of one block, as the kernels want them."""
 
@@ -221,10 +239,19 @@ class UserOptimizedTransformer(nn.Module):
             cache[index] = cached
         return cached[1]
 
+    def _tree(self) -> Tuple[Tuple[nn.Parameter, ...], Tuple[nn.LayerNorm, ...]]:
+        """(parameters, LayerNorm modules) of this model, re-walked after any registration."""
+        cached = self.__dict__.get("_tree_cache")
+        if cached is None or cached[0] != _TREE_GENERATION[0]:
+            cached = (_TREE_GENERATION[0], tuple(self.parameters()),
+                      tuple(m for m in self.modules() if isinstance(m, nn.LayerNorm)))
+            self.__dict__["_tree_cache"] = cached
+        return cached[1], cached[2]
+
     def _uses_fused_stack(self, x: torch.Tensor) -> bool:
         """Shape contract of xb_fused_forward_d128."""
         cfg = self.config
-        norms = [m for m in self.modules() if isinstance(m, nn.LayerNorm)]
+        norms = self._tree()[1]
         return (
             self._fused_stack_enabled
             and cfg.d_model == 128
@@ -236,10 +263,13 @@ class UserOptimizedTransformer(nn.Module):
 
     def _fused_stack_parameters(self) -> Tuple[torch.Tensor, torch.Tensor, int]:
         """Fragment-packed FP16 weights, FP32 bias/LayerNorm buffer and LayerNorm affine mask, cached by version."""
-        params = list(self.parameters())
-        key = tuple((p.data_ptr(), _tensor_version(p), p.device) for p in params)
+        params = self._tree()[0]
+        try:
+            key = (tuple([p._version for p in params]), tuple([p.data_ptr() for p in params]))
+        except RuntimeError:  # inference-mode parameters have no version counter: never reuse
+            key = None
         cached = self.__dict__.get("_fused_stack_cache")
-        if cached is not None and cached[0] == key and all(k[1] is not None for k in key):
+        if key is not None and cached is not None and cached[0] == key:
             return cached[1], cached[2], cached[3]
         weights, vectors = [], []
         with torch.no_grad():
@@ -287,6 +317,22 @@ class UserOptimizedTransformer(nn.Module):
             cached = (key, not is_identity)
             layer_norm._xblock_affine_cache = cached
         return cached[1]
+
+    def _single_launch_forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor]) -> bool:
+        """Whether forward(x, valid_token_mask) is exactly one kernel launch (the whole-stack kernel).
+
+        Such a forward gains nothing from graph replay, which would only add
+        the copy of the static output that every replay returns.
+        """
+        chunk = self._large_batch_chunk_size
+        return (
+            valid_token_mask is None
+            and not self._kv_cache_enabled
+            and x.is_cuda and x.ndim == 3 and x.dtype == torch.float32 and x.is_contiguous()
+            and not (chunk and x.shape[0] > chunk)
+            and self._uses_fused_stack(x)
+            and (self.config.causal or self.config.head_dim <= 64)
+        )
 
     def _all_tokens_valid(self, valid_token_mask: Optional[torch.Tensor], seq_len: int) -> bool:
         """Mask inspection cached by identity + version + length (TTB:464-522)."""

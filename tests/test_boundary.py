@@ -96,6 +96,22 @@ def test_toggles(pkg):
     pkg.UserOptimizedTransformer(pkg.TransformerConfig(1, 4, 32, 4, 32, 1, False)).enable_attention_fp16_accumulation(True)
 
 
+def test_tree_cache_follows_registrations(pkg):
+    """The cached parameter / LayerNorm walk is redone after any parameter or module assignment."""
+    model = pkg.UserOptimizedTransformer(pkg.TransformerConfig(2, 8, 128, 4, 128, 2, True)).eval()
+    x = torch.empty(2, 8, 128)
+    params, norms = model._tree()
+    assert list(params) == list(model.parameters()) and len(norms) == 2 * 2 + 1
+    assert model._tree()[0] is params                      # no registration: the same walk
+    assert model._uses_fused_stack(x) and not model._single_launch_forward(x, None)  # CPU input
+    fresh = torch.nn.Parameter(torch.zeros(128, 128))
+    model.layers[1].ffn_in.weight = fresh
+    assert any(p is fresh for p in model._tree()[0])
+    model.final_norm = torch.nn.LayerNorm(128, eps=1e-6)
+    assert model._tree()[1][-1] is model.final_norm
+    assert not model._uses_fused_stack(x)                  # eps outside the kernel's contract
+
+
 def test_product_never_touches_the_oracle():
     for path in (REPO / "gpu-kernel-for-transformer_amd").rglob("*.py"):
         text = path.read_text()

@@ -207,6 +207,27 @@ def test_graph_replay_matches_eager(pkg, cuda):
             del scratch
 
 
+def test_maybe_cuda_graph_choice(pkg, cuda):
+    """One-kernel forwards stay eager; per-op forwards are captured and replay bitwise; weight updates reach both."""
+    graphs = __import__(pkg.__name__ + ".graph_runner", fromlist=["x"])
+    for config, single in ((pkg.TransformerConfig(4, 64, 128, 4, 128, 2, True), True),
+                           (pkg.TransformerConfig(2, 64, 256, 4, 512, 2, True), False)):
+        _, optimized = _models(pkg, config, cuda)
+        x = torch.randn(config.batch_size, config.seq_len, config.d_model, device=cuda)
+        with torch.inference_mode():
+            runner, graphed, reason = graphs.maybe_cuda_graph(optimized, x, None, enabled=True)
+            assert graphed is (not single) and (runner is optimized) is single, reason
+            first = runner(x).clone()
+            assert torch.equal(first, optimized(x))
+        # An in-place weight update (a new state_dict) is seen by the eager path's caches.
+        state = {k: v.clone() for k, v in optimized.state_dict().items()}
+        state["layers.0.ffn_out.bias"] += 0.5
+        optimized.load_state_dict(state)
+        with torch.inference_mode():
+            second = optimized(x)
+        assert not torch.equal(first, second)
+
+
 def _padded_parity(pkg, cuda, config, x, mask, label):
     baseline, optimized = _models(pkg, config, cuda)
     with torch.inference_mode():
