@@ -408,6 +408,314 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_kernel(const AttnArgs a)
   }
 }
 
+// dma16 issued from inline assembly: the compiler does not see this LDS
+// write, so it adds no wait for it before later LDS reads (it cannot tell the
+// ring buffer being filled from the one being read, and would wait before
+// every read).  The caller waits itself (vmcnt) before the barrier that
+// publishes the tile.  Any wait the compiler does emit for its own loads only
+// waits longer, since it counts fewer operations in flight than there are.
+__device__ __forceinline__ void dma16_untracked(const void* src_lane, void* lds_wave_base) {
+  const uint32_t lds = (uint32_t)(uintptr_t)(lds_void_t*)lds_wave_base;
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src_lane), "s"(lds) : "memory", "m0");
+}
+
+// Ping-pong variant for long sequences (head_dim 64, no key mask): 8 waves in
+// two groups of four, A = waves 0-3 and B = waves 4-7, one wave of each per
+// SIMD.  Per 64-key tile a wave runs an MFMA phase (PV of the previous tile,
+// then QK of this one) and a VALU phase (mask, offset check, exp2 and FP16
+// packing of the probabilities).  Barriers split time into half-steps, and
+// the groups take opposite phases in each: in half-step 2t group A does
+// PV(t-1) + QK(t) while group B does the VALU work of tile t-1; in 2t+1 A does
+// the VALU work of tile t while B does PV(t-1) + QK(t).  So on every SIMD one
+// wave keeps the matrix core busy while the other issues the exponentials,
+// instead of both waves reaching the same phase at once.
+//
+// K/V tiles sit in a ring of three LDS buffers (tile t in buffer t % 3) and
+// arrive by direct global -> LDS loads (no VGPRs in between).  Tile t is read
+// from half-step 2t (A's QK) to 2t+3 (B's PV); the loads of tile t+1 are
+// issued in half-step 2t (into the buffer of tile t-2, last read in 2t-1) and
+// waited for at the end of 2t+1.  Rows are 128 bytes, unpadded
+// (a load fills 1 KB = 8 rows contiguously); chunk c of row r sits in slot
+// c ^ (r & 7), applied on the global side, which keeps the K fragment reads
+// and the transposing V reads free of bank conflicts.  Same arithmetic as
+// attn_kernel (offset in the score accumulator, lazy rescale, MFMA row sums).
+template <int HD, bool CAUSAL>
+__global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
+  constexpr int NQ = 4, NW = 8;
+  using C = AttnCfg<HD, NQ, NW>;
+  constexpr int NT = C::NT, BKEYS = C::BKEYS, QPW = C::QPW, BQ = C::BQ;
+  constexpr int LDK = C::LDK, LDV = C::LDV, KSTEPS = C::KSTEPS, KB = C::KB, HB = C::HB;
+  constexpr int KT = C::KT, CPK = C::CPK, CH = C::CH;
+  static_assert(HD == 64 && C::HDP == 64 && C::HDV == 64, "128-byte rows");
+  static_assert(BKEYS == 8 * NW, "one 8-row load per wave per tile");
+  constexpr int NBUF = 3;
+  constexpr int ROW = HD;  // halves per LDS row
+
+  __shared__ __attribute__((aligned(1024))) half_t k_lds[NBUF][BKEYS * ROW];
+  __shared__ __attribute__((aligned(1024))) half_t v_lds[NBUF][BKEYS * ROW];
+  // Q operands, fragment-major (wave, qb, ks, lane): re-read per tile rather
+  // than held in 32 VGPRs, which two waves per SIMD cannot spare.
+  __shared__ __attribute__((aligned(16))) half8_t q_lds[NW][NQ][KSTEPS][kWave];
+
+  const int per_bh = a.q_tiles;
+  const int bh = blockIdx.x / per_bh;
+  const int sub = blockIdx.x % per_bh;
+  const int qt = CAUSAL ? a.q_tiles - 1 - sub : sub;  // heaviest query tiles first
+  const int b = bh / a.H, h = bh % a.H;
+  const int S_q = a.S_q, S_k = a.S_k, q_offset = a.q_offset;
+  const half_t* base = a.q + (int64_t)b * a.q_bstride + (int64_t)h * HD;
+  const int64_t q_rstride = a.q_rstride, k_rstride = a.k_rstride;
+  const half_t* kbase = a.k + (int64_t)b * a.k_bstride + (int64_t)h * a.k_hstride;
+  const half_t* vbase = a.v + (int64_t)b * a.k_bstride + (int64_t)h * a.k_hstride;
+  const float scale_log2 = a.scale_log2;
+
+  const int tid = threadIdx.x, lane = tid % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int g = lane / 16, r16 = lane % 16;
+  const int q0 = qt * BQ;
+  const int qw0 = q0 + wave * QPW;
+  // Waves w and w + 4 share a SIMD (measured: pairing them by the SIMD id in
+  // HW_ID gives the same time; pairing w and w + 1 runs 1.6x slower).  Only
+  // the schedule depends on it, not the result.
+  const bool group_a = wave < NW / 2;
+
+  const half8_t zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int qb = 0; qb < NQ; ++qb) {
+    const int q = qw0 + 16 * qb + r16;
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+      half8_t v = zero8;
+      if (q < S_q) {
+        v = *reinterpret_cast<const half8_t*>(base + q * q_rstride + 32 * ks + 8 * g);
+#pragma unroll
+        for (int m = 0; m < 8; ++m) v[m] = (half_t)((float)v[m] * scale_log2);
+      }
+      q_lds[wave][qb][ks][lane] = v;  // read back only by this wave, after the first barrier
+    }
+  }
+  float4_t o[HB][NQ], lacc[NQ];
+  float m_run[NQ];
+#pragma unroll
+  for (int qb = 0; qb < NQ; ++qb) {
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb) o[hb][qb] = float4_t{0.f, 0.f, 0.f, 0.f};
+    lacc[qb] = float4_t{0.f, 0.f, 0.f, 0.f};
+    m_run[qb] = 0.f;
+  }
+  const half8_t ones8 = {1, 1, 1, 1, 1, 1, 1, 1};
+
+  // Tile loads: wave w fills rows 8w .. 8w+7 of the K and V buffers; lane i
+  // fetches the chunk that belongs in slot i % 8 of row i / 8.  Rows past S_k
+  // repeat row S_k - 1: those keys are masked (causal: they follow every
+  // query; otherwise explicitly), so their probabilities are exactly 0, and a
+  // real row is finite.
+  const int ld_row = 8 * wave + lane / 8, ld_chunk = (lane % 8) ^ (lane / 8);
+  auto dma_tile = [&](int t) {  // tile t into buffer t % NBUF
+    const int64_t off = (int64_t)min(t * BKEYS + ld_row, S_k - 1) * k_rstride + 8 * ld_chunk;
+    const int buf = t % NBUF;
+    dma16_untracked(kbase + off, &k_lds[buf][8 * wave * ROW]);
+    dma16_untracked(vbase + off, &v_lds[buf][8 * wave * ROW]);
+  };
+  // Barrier over LDS traffic only: the next tile's loads stay in flight ...
+  auto half_step_barrier = [] {
+    __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // vmcnt(63) expcnt(7) lgkmcnt(0)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  // ... except at the end of odd half-steps, where they must have landed.
+  auto tile_barrier = [] {
+    __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (0 << 8) | (0 << 14));  // vmcnt(0) expcnt(7) lgkmcnt(0)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+
+  int key_end = CAUSAL ? min(S_k, q_offset + q0 + BQ) : S_k;
+  const int n_tiles = (key_end + BKEYS - 1) / BKEYS;
+  // Tiles past this wave's last query (causal) are skipped by the wave, not by
+  // the workgroup: every wave passes every barrier.
+  auto active = [&](int t) { return t >= 0 && t < n_tiles && (!CAUSAL || t * BKEYS <= q_offset + qw0 + QPW - 1); };
+
+  float4_t s[KB][NQ];
+  half8_t pf[KT][NQ];
+
+  // QK of tile t into s (offset already subtracted).
+  // Lane parts of the LDS addresses come from opaque copies inside each call,
+  // so they stay one base register plus instruction offsets instead of being
+  // hoisted out of the tile loop as one register per fragment (and spilled).
+  auto mma_qk = [&](int t) {
+    // Row 16 jb + r16, chunk 4 ks + g, in slot (4 ks + g) ^ (r16 & 7).
+    int ql = lane, kc = g ^ (r16 & 7), kr = r16 * ROW;
+    asm volatile("" : "+v"(ql), "+v"(kc), "+v"(kr));
+    const half_t* kt_lds = k_lds[t % NBUF];
+    const half_t* kp[KSTEPS] = {kt_lds + kr + 8 * kc, kt_lds + kr + 8 * (kc ^ 4)};
+    half8_t qf[NQ][KSTEPS];
+#pragma unroll
+    for (int qb = 0; qb < NQ; ++qb)
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks) qf[qb][ks] = q_lds[wave][qb][ks][ql];
+#pragma unroll
+    for (int jb = 0; jb < KB; ++jb) {
+#pragma unroll
+      for (int qb = 0; qb < NQ; ++qb) s[jb][qb] = float4_t{-m_run[qb], -m_run[qb], -m_run[qb], -m_run[qb]};
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks) {
+        const half8_t kf = *reinterpret_cast<const half8_t*>(kp[ks] + 16 * jb * ROW);
+#pragma unroll
+        for (int qb = 0; qb < NQ; ++qb) s[jb][qb] = mfma16x16x32(kf, qf[qb][ks], s[jb][qb]);
+      }
+    }
+  };
+  // O^T += V^T . P^T of tile t (and the row sums).
+  auto mma_pv = [&](int t) {
+    // Lane (g, j) reads 8 bytes of row 32 kt + 4 g + j / 4 (+16 for the high
+    // half) at half 4 (j % 4) + 16 hb: chunk 2 hb + (j % 4) / 2, which sits in
+    // slot chunk ^ (row & 7) = cb ^ 2 hb.
+    int vr = (4 * g + r16 / 4) * ROW + 4 * (r16 % 2), cb = ((r16 % 4) / 2) ^ ((4 * g + r16 / 4) & 7);
+    asm volatile("" : "+v"(vr), "+v"(cb));
+    const half_t* vt_lds = v_lds[t % NBUF] + vr;
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+#pragma unroll
+      for (int qb = 0; qb < NQ; ++qb) lacc[qb] = mfma16x16x32(ones8, pf[kt][qb], lacc[qb]);
+      const half_t* vrow = vt_lds + 32 * kt * ROW;
+#pragma unroll
+      for (int hb = 0; hb < HB; ++hb) {
+        const int slot = 8 * (cb ^ (2 * hb));
+        const half4_t lo = lds_read_tr16(vrow + slot);
+        const half4_t hi = lds_read_tr16(vrow + 16 * ROW + slot);
+        const half8_t vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+        for (int qb = 0; qb < NQ; ++qb) o[hb][qb] = mfma16x16x32(vf, pf[kt][qb], o[hb][qb]);
+      }
+    }
+  };
+  // Mask, offset check / rescale, probabilities of tile t.
+  auto softmax = [&](int t) {
+    const int k0 = t * BKEYS;
+    // The mask thresholds below come from opaque copies of the lane
+    // coordinates: otherwise the compiler hoists all 64 lane constants out of
+    // the tile loop and spills them.
+    int g = lane / 16, r16 = lane % 16;
+    asm volatile("" : "+v"(g), "+v"(r16));
+    // One key block at a time: formed all at once, the 64 compare masks would
+    // need 128 SGPRs.
+    if (CAUSAL && k0 + BKEYS - 1 > q_offset + qw0) {
+      const int d = 4 * g - r16 + k0 - q_offset - qw0;  // key - query of element (0, 0, 0)
+#pragma unroll
+      for (int jb = 0; jb < KB; ++jb) {
+#pragma unroll
+        for (int qb = 0; qb < NQ; ++qb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (d + 16 * jb + i > 16 * qb) s[jb][qb][i] = -INFINITY;
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else if (!CAUSAL && k0 + BKEYS > S_k) {
+#pragma unroll
+      for (int jb = 0; jb < KB; ++jb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (k0 + 16 * jb + 4 * g + i >= S_k)
+#pragma unroll
+            for (int qb = 0; qb < NQ; ++qb) s[jb][qb][i] = -INFINITY;
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    float lm = -INFINITY;
+#pragma unroll
+    for (int qb = 0; qb < NQ; ++qb)
+#pragma unroll
+      for (int jb = 0; jb < KB; ++jb)
+        lm = fmaxf(lm, fmaxf(fmaxf(s[jb][qb][0], s[jb][qb][1]), fmaxf(s[jb][qb][2], s[jb][qb][3])));
+    if (__any(t == 0 || lm > 8.0f)) {
+#pragma unroll
+      for (int qb = 0; qb < NQ; ++qb) {
+        float m = -INFINITY;
+#pragma unroll
+        for (int jb = 0; jb < KB; ++jb)
+          m = fmaxf(m, fmaxf(fmaxf(s[jb][qb][0], s[jb][qb][1]), fmaxf(s[jb][qb][2], s[jb][qb][3])));
+        const float mx = quad_group_max(m);
+        // Tile 0 shows every query key 0, so its maximum is finite: the offset
+        // jumps there with nothing to rescale; later sh >= 0 and corr <= 1.
+        const float sh = t != 0 ? fmaxf(mx, 0.f) : mx;
+        const float corr = t != 0 ? __builtin_amdgcn_exp2f(-sh) : 1.f;
+        m_run[qb] += sh;
+#pragma unroll
+        for (int hb = 0; hb < HB; ++hb) o[hb][qb] *= corr;
+        lacc[qb] *= corr;
+#pragma unroll
+        for (int jb = 0; jb < KB; ++jb) s[jb][qb] -= sh;
+      }
+    }
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+      for (int qb = 0; qb < NQ; ++qb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          pf[kt][qb][i] = (half_t)__builtin_amdgcn_exp2f(s[2 * kt][qb][i]);
+          pf[kt][qb][4 + i] = (half_t)__builtin_amdgcn_exp2f(s[2 * kt + 1][qb][i]);
+        }
+  };
+  auto mfma_phase = [&](int t) {
+    __builtin_amdgcn_s_setprio(1);
+    if (active(t - 1)) mma_pv(t - 1);
+    // The probabilities die before the scores are born: no interleaving of
+    // the two products, which would need both live (96 more VGPRs).
+    __builtin_amdgcn_sched_barrier(0);
+    if (active(t)) mma_qk(t);
+    __builtin_amdgcn_s_setprio(0);
+  };
+
+  if (n_tiles > 0) dma_tile(0);
+  __builtin_amdgcn_s_waitcnt(0);  // tile 0 and the Q operands have landed
+  __syncthreads();
+  // The two groups run separate copies of the loop, each passing the same
+  // 2 (n_tiles + 1) barriers, rotated so that only the probabilities (not the
+  // scores) cross the back edge.  Every wave issues its share of tile t+1's
+  // loads at the start of half-step 2t (group B: at the end of its softmax,
+  // once its PV of tile t-2 is done) and waits for them at the end of 2t+1.
+  if (group_a) {
+    for (int t = 0; t <= n_tiles; ++t) {
+      if (t + 1 < n_tiles) dma_tile(t + 1);
+      mfma_phase(t);  // half-step 2t: PV(t-1) + QK(t)
+      half_step_barrier();
+      if (active(t)) softmax(t);  // half-step 2t+1
+      tile_barrier();
+    }
+  } else {
+    if (1 < n_tiles) dma_tile(1);
+    half_step_barrier();  // half-step 0: nothing to exponentiate yet
+    for (int t = 0; t < n_tiles; ++t) {
+      mfma_phase(t);  // half-step 2t+1: PV(t-1) + QK(t)
+      tile_barrier();
+      if (t + 2 < n_tiles) dma_tile(t + 2);
+      if (active(t)) softmax(t);  // half-step 2t+2
+      half_step_barrier();
+    }
+    mfma_phase(n_tiles);  // half-step 2 n_tiles + 1: PV of the last tile
+    tile_barrier();
+  }
+
+  half_t* obase = a.out + (int64_t)b * a.o_bstride + (int64_t)h * HD;
+#pragma unroll
+  for (int qb = 0; qb < NQ; ++qb) {
+    const float inv = lacc[qb][0] > 0.f ? __builtin_amdgcn_rcpf(lacc[qb][0]) : 0.f;
+    const int q = qw0 + 16 * qb + r16;
+    if (q >= S_q) continue;
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb) {
+      half4_t r;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) r[i] = (half_t)(o[hb][qb][i] * inv);
+      *reinterpret_cast<half4_t*>(obase + (int64_t)q * a.o_rstride + 16 * hb + 4 * g) = r;
+    }
+  }
+}
+
 // Merges the key-range partials of attn_kernel<..., SPLIT>: per (batch, head,
 // query) M = max_s m_s, out = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s.
 // One thread per 8 context columns.
@@ -468,8 +776,25 @@ static hipError_t launch_attn(AttnArgs a, int B, int causal, hipStream_t s) {
   return hipGetLastError();
 }
 
-// Long query ranges take 64 queries per wave (each K/V fragment read from LDS
-// then feeds 4 MFMAs); short ones keep 32 so a block does not outgrow S_q.
+template <int HD>
+static hipError_t launch_attn_pp(AttnArgs a, int B, int causal, hipStream_t s) {
+  constexpr int BQ = AttnCfg<HD, 4, 8>::BQ;
+  a.q_tiles = (a.S_q + BQ - 1) / BQ;
+  const int64_t blocks = (int64_t)a.q_tiles * B * a.H;
+  if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
+  if (causal)
+    hipLaunchKernelGGL((attn_pp_kernel<HD, true>), dim3((unsigned)blocks), dim3(512), 0, s, a);
+  else
+    hipLaunchKernelGGL((attn_pp_kernel<HD, false>), dim3((unsigned)blocks), dim3(512), 0, s, a);
+  return hipGetLastError();
+}
+
+// Query ranges of at least kPingPongMinQueries (head_dim 64, no key mask) take
+// the ping-pong kernel (512 queries per block); other long ranges take 64
+// queries per wave (each K/V fragment read from LDS then feeds 4 MFMAs);
+// short ones keep 32 so a block does not outgrow S_q.
+constexpr int kPingPongMinQueries = 4096;
+
 template <int HD>
 static hipError_t dispatch_attn(const AttnArgs& a, int B, int causal, hipStream_t s) {
   if constexpr (HD >= 256) {
@@ -477,6 +802,9 @@ static hipError_t dispatch_attn(const AttnArgs& a, int B, int causal, hipStream_
   } else if constexpr (HD >= 128) {
     return launch_attn<HD, 2>(a, B, causal, s);
   } else {
+    if constexpr (HD == 64) {
+      if (a.key_valid == nullptr && a.S_q >= kPingPongMinQueries) return launch_attn_pp<HD>(a, B, causal, s);
+    }
     if (a.S_q >= 1024) return launch_attn<HD, 4>(a, B, causal, s);
     return launch_attn<HD, 2>(a, B, causal, s);
   }

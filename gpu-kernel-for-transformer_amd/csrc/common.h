@@ -89,4 +89,14 @@ __device__ __forceinline__ float xor32_max(float v) {
 __device__ __forceinline__ float quad_group_sum(float v) { return xor32_sum(xor16_sum(v)); }
 __device__ __forceinline__ float quad_group_max(float v) { return xor32_max(xor16_max(v)); }
 
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void global_void_t;
+
+// One 16-byte-per-lane direct global -> LDS load (global_load_lds_dwordx4):
+// lane i's bytes land at lds_wave_base + 16 i.  The LDS base must be
+// wave-uniform; completion is counted by vmcnt.
+__device__ __forceinline__ void dma16(const void* src_lane, void* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds((global_void_t*)src_lane, (lds_void_t*)lds_wave_base, 16, 0, 0);
+}
+
 }  // namespace xb

@@ -100,15 +100,6 @@ __device__ __forceinline__ void layer_norm(const float4_t (&res)[FB], const floa
   }
 }
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) void global_void_t;
-
-// One 16-byte-per-lane direct global -> LDS load: lane i's bytes land at
-// lds_wave_base + 16 i.  The LDS base must be wave-uniform.
-__device__ __forceinline__ void dma16(const void* src_lane, void* lds_wave_base) {
-  __builtin_amdgcn_global_load_lds((global_void_t*)src_lane, (lds_void_t*)lds_wave_base, 16, 0, 0);
-}
-
 // Workgroup barrier after this wave's DMA loads and LDS accesses completed.
 // (__syncthreads would also do; spelled out because the waits matter.)
 __device__ __forceinline__ void drain_and_barrier() {

@@ -165,8 +165,6 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_nt_kernel(
 // 8 distinct 16-byte bank groups.  A DMA load writes lane i's 16 bytes to
 // consecutive LDS addresses, so the swizzle is applied on the global side:
 // lane i of a 1 KB segment (8 rows) fetches the chunk that belongs in its slot.
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) void global_void_t;
 
 
 // s_waitcnt with vmcnt <= N and lgkmcnt == 0 (gfx9 field layout:

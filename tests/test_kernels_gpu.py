@@ -153,6 +153,23 @@ def test_causal_attention_long(pkg, cuda, hd, s):
     torch.testing.assert_close(out.cpu().float(), ref, atol=2e-3, rtol=1e-2)
 
 
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("b,s,h", [(2, 4096, 2), (1, 4133, 3), (1, 8703, 1)])
+def test_attention_long_hd64_ping_pong(pkg, cuda, b, s, h, causal):
+    """head_dim 64, S >= 4096, no mask: the ping-pong kernel (two wave groups, K/V
+    ring loaded straight into LDS).  FP32 reference, and bitwise equal to the
+    four-wave kernel, which an all-valid key mask selects: same 64-query waves,
+    same tile order and the same wave-uniform rescale decisions."""
+    hd = 64
+    qkv = torch.randn(b, s, 3 * h * hd, generator=_gen(s + h)).half()
+    ref = _attention_reference(qkv, h, causal=causal)
+    qg = qkv.to(cuda)
+    out = pkg.attention(qg, h, causal=causal)
+    torch.testing.assert_close(out.cpu().float(), ref, atol=2e-3, rtol=1e-2)
+    ones = torch.ones(b, s, dtype=torch.bool, device=cuda)
+    assert torch.equal(out, pkg.attention(qg, h, key_valid=ones, causal=causal))
+
+
 def test_causal_attention_first_token_is_value(pkg, cuda):
     """Query 0 sees only key 0, so its context equals v[0] exactly (up to FP16)."""
     qkv = torch.randn(3, 50, 3 * 4 * 32, generator=_gen(9)).half()
@@ -208,13 +225,14 @@ def test_attention_all_valid_mask_equals_unmasked(pkg, cuda):
 
 
 @pytest.mark.parametrize("causal", [True, False])
-def test_attention_large_negative_first_scores(pkg, cuda, causal):
+@pytest.mark.parametrize("long_s", [False, True])  # True: the ping-pong kernel
+def test_attention_large_negative_first_scores(pkg, cuda, causal, long_s):
     """First key tile scores far below zero (2^-185 probabilities before the shift).
 
     The running offset must jump onto them without rescaling the still-empty
     accumulators by exp2(185) (= inf, and 0 * inf = NaN).
     """
-    b, s, h, hd = 1, 192, 1, 64
+    b, s, h, hd = 1, 192 if long_s is False else 4160, 1, 64
     q = torch.full((s, hd), 4.0)
     k = torch.full((s, hd), 0.05)
     k[:64] = -4.0                      # q.k * scale * log2(e) = -184.7 for keys 0..63
