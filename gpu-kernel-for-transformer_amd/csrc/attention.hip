@@ -755,23 +755,23 @@ __global__ __launch_bounds__(256) void attn_split_combine(const AttnArgs a, int 
                               (int64_t)h * HD + 8 * c) = r;
 }
 
-template <int HD, int NQ>
+template <int HD, int NQ, int NW = 4>
 static hipError_t launch_attn(AttnArgs a, int B, int causal, hipStream_t s) {
-  constexpr int BQ = AttnCfg<HD, NQ>::BQ;
+  constexpr int BQ = AttnCfg<HD, NQ, NW>::BQ;
   a.q_tiles = (a.S_q + BQ - 1) / BQ;
   const int64_t blocks = (int64_t)a.q_tiles * B * a.H;
   if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
-  const dim3 grid((unsigned)blocks), block(AttnCfg<HD, NQ>::NT);
+  const dim3 grid((unsigned)blocks), block(AttnCfg<HD, NQ, NW>::NT);
   if (a.key_valid != nullptr) {
     if (causal)
-      hipLaunchKernelGGL((attn_kernel<HD, NQ, 4, true, true, false>), grid, block, 0, s, a);
+      hipLaunchKernelGGL((attn_kernel<HD, NQ, NW, true, true, false>), grid, block, 0, s, a);
     else
-      hipLaunchKernelGGL((attn_kernel<HD, NQ, 4, false, true, false>), grid, block, 0, s, a);
+      hipLaunchKernelGGL((attn_kernel<HD, NQ, NW, false, true, false>), grid, block, 0, s, a);
   } else {
     if (causal)
-      hipLaunchKernelGGL((attn_kernel<HD, NQ, 4, true, false, false>), grid, block, 0, s, a);
+      hipLaunchKernelGGL((attn_kernel<HD, NQ, NW, true, false, false>), grid, block, 0, s, a);
     else
-      hipLaunchKernelGGL((attn_kernel<HD, NQ, 4, false, false, false>), grid, block, 0, s, a);
+      hipLaunchKernelGGL((attn_kernel<HD, NQ, NW, false, false, false>), grid, block, 0, s, a);
   }
   return hipGetLastError();
 }
@@ -794,10 +794,16 @@ static hipError_t launch_attn_pp(AttnArgs a, int B, int causal, hipStream_t s) {
 // queries per wave (each K/V fragment read from LDS then feeds 4 MFMAs);
 // short ones keep 32 so a block does not outgrow S_q.
 constexpr int kPingPongMinQueries = 4096;
+constexpr int kCUs = 256;  // MI355X compute units
 
 template <int HD>
 static hipError_t dispatch_attn(const AttnArgs& a, int B, int causal, hipStream_t s) {
   if constexpr (HD >= 256) {
+    // Up to 128 queries: one 8-wave block takes all of them, so each K/V row
+    // is fetched once per (batch, head) instead of by two 64-query blocks
+    // (cfg3's geometry: 16.7 vs 18.6 us) -- when the B*H blocks still fill
+    // the GPU.
+    if (a.S_q <= 128 && (int64_t)B * a.H >= kCUs) return launch_attn<HD, 1, 8>(a, B, causal, s);
     return launch_attn<HD, 1>(a, B, causal, s);
   } else if constexpr (HD >= 128) {
     return launch_attn<HD, 2>(a, B, causal, s);

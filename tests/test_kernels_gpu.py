@@ -170,6 +170,26 @@ def test_attention_long_hd64_ping_pong(pkg, cuda, b, s, h, causal):
     assert torch.equal(out, pkg.attention(qg, h, key_valid=ones, causal=causal))
 
 
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("masked", [False, True])
+def test_attention_hd256_short_one_block_per_head(pkg, cuda, causal, masked):
+    """cfg3's geometry (B*H = 256 heads of S = 128, head_dim 256) takes one 8-wave
+    block per head; slices of two sequences (8 heads) take the 4-wave blocks.
+    Same per-wave work, so the two must agree bitwise; FP32 reference too."""
+    b, s, h, hd = 64, 128, 4, 256
+    qkv = torch.randn(b, s, 3 * h * hd, generator=_gen(256 + causal)).half()
+    valid = _padding_mask(b, s, "random_with_empty", 3) if masked else None
+    qg = qkv.to(cuda)
+    vg = None if valid is None else valid.to(cuda)
+    whole = pkg.attention(qg, h, key_valid=vg, causal=causal)
+    for i in range(0, b, 2):
+        part = pkg.attention(qg[i:i + 2].contiguous(), h, causal=causal,
+                             key_valid=None if vg is None else vg[i:i + 2].contiguous())
+        assert torch.equal(whole[i:i + 2], part), i
+    ref = _attention_reference(qkv[:8], h, key_valid=None if valid is None else valid[:8], causal=causal)
+    torch.testing.assert_close(whole[:8].cpu().float(), ref, atol=2e-3, rtol=1e-2)
+
+
 def test_causal_attention_first_token_is_value(pkg, cuda):
     """Query 0 sees only key 0, so its context equals v[0] exactly (up to FP16)."""
     qkv = torch.randn(3, 50, 3 * 4 * 32, generator=_gen(9)).half()
