@@ -9,9 +9,10 @@
 //   ... ; y = LN_final(x)
 // with FP16 MFMA operands, FP32 accumulation, FP32 residual and softmax.
 //
-// Two kernels: fused_stack_kernel below (eight waves, used for head_dim 128)
-// and the sixteen-wave fused_stack16_kernel further down (head_dim <= 64),
-// which splits each token block's output features between two waves.
+// Two kernels, both eight waves: fused_stack_kernel below (one token block
+// and all features per wave, used for head_dim 128) and fused_stack8x2_kernel
+// further down (head_dim <= 64: two token blocks and half the features per
+// wave).
 //
 // Layout (eight-wave kernel).  Eight waves (two per SIMD) each own one 16-token block: wave w
 // holds block w for w < 4 and block 11-w otherwise, so the two waves sharing
@@ -402,37 +403,19 @@ __global__ __launch_bounds__(64 * NW, 1) void fused_stack_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Sixteen-wave variant (head_dim <= 64).  Each token block is shared by two
-// waves that split every product's OUTPUT features: wave half h owns feature
-// blocks 4h .. 4h+3, which are k-steps 2h, 2h+1 of the next product's operand
-// and the heads inside them.  Four waves per SIMD instead of two hide the
-// MFMA -> softmax / GELU / LayerNorm -> MFMA dependency chains; the price is
-// an LDS exchange of operand halves (LayerNorm outputs, attention context,
-// FFN hidden) and of LayerNorm partial statistics between the two waves of a
-// block.  The exchanges reuse the K and V^T areas while those are dead.
-namespace w16 {
+// Helpers of the feature-split forms (head_dim <= 64): the two waves that
+// hold a token block split every product's OUTPUT features -- wave half h
+// owns feature blocks 4h .. 4h+3, which are k-steps 2h, 2h+1 of the next
+// product's operand, and the heads inside them -- and exchange operand halves
+// (LayerNorm outputs, attention context, FFN hidden) and LayerNorm partial
+// statistics through LDS.  The exchanges reuse the K and V^T areas while
+// those are dead.
+namespace split {
 
-constexpr int NW = 16;
 constexpr int OB = FB / 2;  // own output feature blocks
 constexpr int OK = KS / 2;  // own k-steps
-static_assert(P_LAYER * 4 == NW * 20 * 16, "layer vectors: 20 lanes x 16 bytes per wave");
-static_assert(2 * D * 4 == NW * 4 * 16, "final LayerNorm vectors: 4 lanes x 16 bytes per wave");
+constexpr int XSTAT = 256;  // LayerNorm partial statistics per norm: 16 lanes x 8 blocks x 2 halves
 static_assert(8 * 2 * OK * 1024 <= SMAX * LD * 2, "an exchange area fits in the K (or V^T) area");
-
-// a[j] += staged-matrix output block (OB*half + j) times the operands act.
-template <bool SWAP>
-__device__ __forceinline__ void stage_gemm_half(const char* st, const half8_t (&act)[KS], float4_t (&a)[OB], int half,
-                                                int lane) {
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    half8_t f[OB];
-#pragma unroll
-    for (int j = 0; j < OB; ++j) f[j] = sfrag(st, (OB * half + j) * KS + ks, lane);
-#pragma unroll
-    for (int j = 0; j < OB; ++j)
-      a[j] = SWAP ? mfma16x16x32(f[j], act[ks], a[j]) : mfma16x16x32(act[ks], f[j], a[j]);
-  }
-}
 
 // Workgroup barrier over LDS traffic only: the weight DMA may stay in flight.
 __device__ __forceinline__ void lds_barrier() {
@@ -442,97 +425,16 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// Mean and rstd of the block's rows from both halves: each wave's (mean, M2)
-// over its 64 features meet in LDS and merge by Chan's pairwise formula
-// (equal counts: M2 = M2a + M2b + (ma - mb)^2 * 32).  Both waves of a pair get
-// bit-identical results (the merge is symmetric).
-__device__ __forceinline__ void split_row_stats(const float4_t (&r)[OB], float2* xs, int wave, int lane, float& mean,
-                                                float& rstd) {
-  float s = 0.f;
-#pragma unroll
-  for (int j = 0; j < OB; ++j) s += (r[j][0] + r[j][1]) + (r[j][2] + r[j][3]);
-  const float ma = quad_group_sum(s) * (1.0f / 64);
-  float q = 0.f;
-#pragma unroll
-  for (int j = 0; j < OB; ++j)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) { const float c = r[j][i] - ma; q += c * c; }
-  const float m2a = quad_group_sum(q);
-  // Addresses from an opaque copy of the lane id: rebuilt here each time
-  // rather than kept live (and spilled, whose reload would wait on vmcnt(0),
-  // i.e. on the weight DMA in flight).
-  int l = lane;
-  asm volatile("" : "+v"(l));
-  if (l < 16) xs[wave * 16 + l] = make_float2(ma, m2a);
-  lds_barrier();
-  const float2 pb = xs[(wave ^ 8) * 16 + l % 16];
-  const float d = pb.x - ma;
-  mean = 0.5f * (ma + pb.x);
-  rstd = __builtin_amdgcn_rsqf(((m2a + pb.y) + d * d * 32.f) * (1.0f / D) + 1e-5f);
-}
-
-// LayerNorm of the wave's half of the block -> its two k-steps of operand.
-// affine (wave-uniform): apply gamma / beta; the host clears it when they are
-// exactly 1 and 0 (the reference skips them then too, TTB:568-596), which
-// changes no bit of the result.
-__device__ __forceinline__ void split_layer_norm(const float4_t (&res)[OB], const float* gamma, const float* beta,
-                                                 bool affine, float2* xs, int wave, int lane, int half, int g,
-                                                 half8_t (&own)[OK]) {
-  float mean, rstd;
-  split_row_stats(res, xs, wave, lane, mean, rstd);
-  const float shift = -mean * rstd;
-  if (affine) {
-#pragma unroll
-    for (int j = 0; j < OK; ++j) {
-      const int ks = OK * half + j;
-      float4_t lo, hi;
-      const float4_t g0 = ld4(gamma + 32 * ks + 4 * g), g1 = ld4(gamma + 32 * ks + 16 + 4 * g);
-      const float4_t b0 = ld4(beta + 32 * ks + 4 * g), b1 = ld4(beta + 32 * ks + 16 + 4 * g);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        lo[i] = fmaf(fmaf(res[2 * j][i], rstd, shift), g0[i], b0[i]);
-        hi[i] = fmaf(fmaf(res[2 * j + 1][i], rstd, shift), g1[i], b1[i]);
-      }
-      own[j] = to_operand(lo, hi);
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < OK; ++j) {
-      float4_t lo, hi;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        lo[i] = fmaf(res[2 * j][i], rstd, shift);
-        hi[i] = fmaf(res[2 * j + 1][i], rstd, shift);
-      }
-      own[j] = to_operand(lo, hi);
-    }
-  }
-}
-
 // Exchange slot of (token block, half, k-step): 1 KB, 16 bytes per lane.
 __device__ __forceinline__ half8_t* xslot(char* area, int tb, int half, int j, int lane) {
   return reinterpret_cast<half8_t*>(area + ((tb * 2 + half) * OK + j) * 1024 + lane * 16);
 }
-__device__ __forceinline__ void put_half(char* area, const half8_t (&own)[OK], half8_t (&full)[KS], int tb, int half,
-                                         int lane) {
-#pragma unroll
-  for (int j = 0; j < OK; ++j) {
-    *xslot(area, tb, half, j, lane) = own[j];
-    full[OK * half + j] = own[j];
-  }
-}
-// After a barrier that follows the partner's put_half.
-__device__ __forceinline__ void get_partner(char* area, half8_t (&full)[KS], int tb, int half, int lane) {
-#pragma unroll
-  for (int j = 0; j < OK; ++j) full[OK * (half ^ 1) + j] = *xslot(area, tb, half ^ 1, j, lane);
-}
-
 struct Lds {
   half_t k[SMAX * LD];                                 // K, or an exchange area
   half_t vt[D * LD];                                   // V^T, or an exchange area
   __attribute__((aligned(1024))) char wst[2][MAT_BYTES];  // weight matrix stages
   float prm[2][P_LAYER];                               // per-layer vectors, by layer parity
-  float2 xstat[2][NW * 16];                            // LayerNorm partial statistics
+  float2 xstat[2][XSTAT];                              // LayerNorm partial statistics (LN1 / LN2)
   uint8_t kval[SMAX];                                  // MASKED: token t may be attended to / is output
 };
 
@@ -651,19 +553,152 @@ __device__ __forceinline__ void attend16(const half_t* k_lds, const half_t* vt_l
   }
 }
 
-// The kernel body for one half (HALF is a compile-time constant so that every
-// register-array index below is static).
-// MASK: 0 causal with every token valid; 1 causal with key validity; 2 no
-// causal mask (validity marks tokens past S, and padding if given).
+}  // namespace split
+
+// ---------------------------------------------------------------------------
+// Eight-wave, two-blocks-per-wave form (head_dim <= 64).  Wave w owns token
+// blocks p = w % 4 and 7 - p and the output feature half w / 4; its partner
+// for the other half is wave w ^ 4, on the same SIMD.  Each weight fragment
+// read from LDS feeds two MFMAs (one per block), and blocks p and 7 - p
+// together cost 9 key blocks of causal attention for every wave.  Against a
+// sixteen-wave layout (one block per wave) this measured 2.5% faster on the
+// B=10000 shape and 5% on the 16-head one: both layouts are bound by the
+// SIMDs' instruction issue (VALU and MFMA in lockstep phases), which the
+// balanced attention and halved LDS traffic only trim.
+namespace w8x2 {
+
+constexpr int NW = 8;
+constexpr int NB = 2;       // token blocks per wave
+static_assert(NW * NB * 16 <= split::XSTAT, "one statistics slot per lane, block and wave");
+static_assert(P_LAYER * 4 == NW * 40 * 16, "layer vectors: 40 lanes x 16 bytes per wave");
+static_assert(2 * D * 4 == NW * 8 * 16, "final LayerNorm vectors: 8 lanes x 16 bytes per wave");
+
+using split::OB;
+using split::OK;
+using split::xslot;
+using split::Lds;
+using split::lds_barrier;
+
+// a[b][j] += staged-matrix output block (OB*half + j) times the operands of block b.
+template <bool SWAP>
+__device__ __forceinline__ void stage_gemm2(const char* st, const half8_t (&act)[NB][KS], float4_t (&a)[NB][OB], int half,
+                                            int lane) {
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    half8_t f[OB];
+#pragma unroll
+    for (int j = 0; j < OB; ++j) f[j] = sfrag(st, (OB * half + j) * KS + ks, lane);
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int j = 0; j < OB; ++j)
+        a[b][j] = SWAP ? mfma16x16x32(f[j], act[b][ks], a[b][j]) : mfma16x16x32(act[b][ks], f[j], a[b][j]);
+  }
+}
+
+// Row statistics of both blocks from both halves, one barrier for the two:
+// each wave's (mean, M2) over its 64 features meet in LDS and merge by Chan's
+// pairwise formula (equal counts: M2 = M2a + M2b + (ma - mb)^2 * 32); both
+// waves of a pair get bit-identical results (the merge is symmetric).
+__device__ __forceinline__ void split_row_stats2(const float4_t (&r)[NB][OB], float2* xs, int wave, int lane,
+                                                 float (&mean)[NB], float (&rstd)[NB]) {
+  float ma[NB], m2a[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < OB; ++j) s += (r[b][j][0] + r[b][j][1]) + (r[b][j][2] + r[b][j][3]);
+    ma[b] = quad_group_sum(s) * (1.0f / 64);
+    float q = 0.f;
+#pragma unroll
+    for (int j = 0; j < OB; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) { const float c = r[b][j][i] - ma[b]; q += c * c; }
+    m2a[b] = quad_group_sum(q);
+  }
+  int l = lane;
+  asm volatile("" : "+v"(l));
+  if (l < 16) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) xs[(wave * NB + b) * 16 + l] = make_float2(ma[b], m2a[b]);
+  }
+  lds_barrier();
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const float2 pb = xs[((wave ^ 4) * NB + b) * 16 + l % 16];
+    const float d = pb.x - ma[b];
+    mean[b] = 0.5f * (ma[b] + pb.x);
+    rstd[b] = __builtin_amdgcn_rsqf(((m2a[b] + pb.y) + d * d * 32.f) * (1.0f / D) + 1e-5f);
+  }
+}
+
+// LayerNorm of the wave's half of both blocks -> their own k-steps of operand.
+__device__ __forceinline__ void split_layer_norm2(const float4_t (&res)[NB][OB], const float* gamma, const float* beta,
+                                                  bool affine, float2* xs, int wave, int lane, int half, int g,
+                                                  half8_t (&own)[NB][OK]) {
+  float mean[NB], rstd[NB];
+  split_row_stats2(res, xs, wave, lane, mean, rstd);
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const float shift = -mean[b] * rstd[b];
+#pragma unroll
+    for (int j = 0; j < OK; ++j) {
+      const int ks = OK * half + j;
+      float4_t lo, hi;
+      if (affine) {
+        const float4_t g0 = ld4(gamma + 32 * ks + 4 * g), g1 = ld4(gamma + 32 * ks + 16 + 4 * g);
+        const float4_t b0 = ld4(beta + 32 * ks + 4 * g), b1 = ld4(beta + 32 * ks + 16 + 4 * g);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          lo[i] = fmaf(fmaf(res[b][2 * j][i], rstd[b], shift), g0[i], b0[i]);
+          hi[i] = fmaf(fmaf(res[b][2 * j + 1][i], rstd[b], shift), g1[i], b1[i]);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          lo[i] = fmaf(res[b][2 * j][i], rstd[b], shift);
+          hi[i] = fmaf(res[b][2 * j + 1][i], rstd[b], shift);
+        }
+      }
+      own[b][j] = to_operand(lo, hi);
+    }
+  }
+}
+
+// Own k-steps of both blocks into their exchange slots and into `full`.
+__device__ __forceinline__ void put_half2(char* area, const half8_t (&own)[NB][OK], half8_t (&full)[NB][KS],
+                                          const int (&tb)[NB], int half, int lane) {
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int j = 0; j < OK; ++j) {
+      *xslot(area, tb[b], half, j, lane) = own[b][j];
+      full[b][OK * half + j] = own[b][j];
+    }
+}
+// After a barrier that follows the partner's put_half2.
+__device__ __forceinline__ void get_partner2(char* area, half8_t (&full)[NB][KS], const int (&tb)[NB], int half,
+                                             int lane) {
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int j = 0; j < OK; ++j) full[b][OK * (half ^ 1) + j] = *xslot(area, tb[b], half ^ 1, j, lane);
+}
+
+// Causal attention of blocks P and 7 - P (MASK 2: no causal mask) for the heads of half HALF.
+template <int HD, int HALF, int P, int MASK>
+__device__ __forceinline__ void attend_pair(const Lds& L, const half8_t (&qop)[NB][OK], half8_t (&cop)[NB][KS], int g,
+                                            int r16) {
+  split::attend16<HD, HALF, P, MASK>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16);
+  split::attend16<HD, HALF, 7 - P, MASK>(L.k, L.vt, L.kval, qop[1], cop[1], g, r16);
+}
+
 template <int HD, int HALF, int MASK>
-__device__ __forceinline__ void stack16_body(Lds& L, const float* __restrict__ x, float* __restrict__ y,
-                                             const half_t* __restrict__ wpack, const float* __restrict__ ppack,
-                                             int S, int layers, int64_t affine_mask, int wave, int tb) {
+__device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ x, float* __restrict__ y,
+                                              const half_t* __restrict__ wpack, const float* __restrict__ ppack,
+                                              int S, int layers, int64_t affine_mask, int wave, int pair) {
   constexpr int H = D / HD;
   static_assert(H >= 2, "heads split between the two halves");
-  constexpr int HH = H / 2;                    // heads per half
-  constexpr int HDB = HD < 16 ? 1 : HD / 16;   // 16-row blocks of one head in V^T
-  constexpr int KSH = HD >= 32 ? HD / 32 : 1;  // k-steps of one head's q.k
   constexpr int half = HALF;
   half_t* const k_lds = L.k;
   half_t* const vt_lds = L.vt;
@@ -678,6 +713,7 @@ __device__ __forceinline__ void stack16_body(Lds& L, const float* __restrict__ x
   const int64_t seq = blockIdx.x;
   const float* xs = x + seq * S * D;
   const int groups = layers * MATS;
+  const int tb[NB] = {pair, 7 - pair};
 
   auto issue_group = [&](int gi) {
     const int layer = gi / MATS, m = gi % MATS;
@@ -690,9 +726,9 @@ __device__ __forceinline__ void stack16_body(Lds& L, const float* __restrict__ x
     if (m == MATS - 1) {
       float* dst = prm[(layer + 1) & 1];
       if (layer + 1 < layers) {
-        if (lane < 20) dma16(ppack + (int64_t)(layer + 1) * P_LAYER + wave * 80 + lane * 4, dst + wave * 80);
+        if (lane < 40) dma16(ppack + (int64_t)(layer + 1) * P_LAYER + wave * 160 + lane * 4, dst + wave * 160);
       } else {
-        if (lane < 4) dma16(ppack + (int64_t)layers * P_LAYER + wave * 16 + lane * 4, dst + wave * 16);
+        if (lane < 8) dma16(ppack + (int64_t)layers * P_LAYER + wave * 32 + lane * 4, dst + wave * 32);
       }
     }
   };
@@ -702,137 +738,161 @@ __device__ __forceinline__ void stack16_body(Lds& L, const float* __restrict__ x
     return wst[gi & 1];
   };
 
-  // Residual stream, own half: res[j][i] = x[16 tb + r16][16 (OB half + j) + 4 g + i].
-  float4_t res[OB];
-  const int tok = 16 * tb + r16;
+  // Residual stream, own half of both blocks: res[b][j][i] = x[16 tb[b] + r16][16 (OB half + j) + 4 g + i].
+  float4_t res[NB][OB];
 #pragma unroll
-  for (int j = 0; j < OB; ++j)
-    res[j] = tok < S ? ld4(xs + (int64_t)tok * D + 16 * (OB * half + j) + 4 * g) : float4_t{0.f, 0.f, 0.f, 0.f};
-  if (lane < 20) dma16(ppack + wave * 80 + lane * 4, prm[0] + wave * 80);
+  for (int b = 0; b < NB; ++b) {
+    const int tok = 16 * tb[b] + r16;
+#pragma unroll
+    for (int j = 0; j < OB; ++j)
+      res[b][j] = tok < S ? ld4(xs + (int64_t)tok * D + 16 * (OB * half + j) + 4 * g) : float4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  if (lane < 40) dma16(ppack + wave * 160 + lane * 4, prm[0] + wave * 160);
   issue_group(0);
   drain_and_barrier();
 
   for (int layer = 0; layer < layers; ++layer) {
     const float* pp = prm[layer & 1];
     const int g0 = layer * MATS;
-    half8_t xn[KS];
+    half8_t xn[NB][KS];
     {
-      half8_t own[OK];
-      split_layer_norm(res, pp + P_G1, pp + P_BE1, (affine_mask >> min(2 * layer, 63)) & 1, xstat[0], wave, lane, half, g,
-                       own);
-      put_half(area_a, own, xn, tb, half, lane);
+      half8_t own[NB][OK];
+      split_layer_norm2(res, pp + P_G1, pp + P_BE1, (affine_mask >> min(2 * layer, 63)) & 1, xstat[0], wave, lane,
+                        half, g, own);
+      put_half2(area_a, own, xn, tb, half, lane);
     }
 
     // ---- Q (own heads), kept in registers --------------------------------
-    half8_t qop[OK];
+    half8_t qop[NB][OK];
     {
       const char* st = begin_group(g0 + 0);
-      get_partner(area_a, xn, tb, half, lane);
-      float4_t qc[OB];
+      get_partner2(area_a, xn, tb, half, lane);
+      float4_t qc[NB][OB];
 #pragma unroll
-      for (int j = 0; j < OB; ++j) qc[j] = ld4(pp + P_BQ + 16 * (OB * half + j) + 4 * g);
-      stage_gemm_half<true>(st, xn, qc, half, lane);
+      for (int b = 0; b < NB; ++b)
 #pragma unroll
-      for (int j = 0; j < OK; ++j) qop[j] = to_operand(qc[2 * j], qc[2 * j + 1]);
+        for (int j = 0; j < OB; ++j) qc[b][j] = ld4(pp + P_BQ + 16 * (OB * half + j) + 4 * g);
+      stage_gemm2<true>(st, xn, qc, half, lane);
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int j = 0; j < OK; ++j) qop[b][j] = to_operand(qc[b][2 * j], qc[b][2 * j + 1]);
     }
     // ---- K (own features) -> LDS, permuted per k-step ----------------------
     {
       const char* st = begin_group(g0 + 1);
-      float4_t a[OB];
+      float4_t a[NB][OB];
 #pragma unroll
-      for (int j = 0; j < OB; ++j) a[j] = ld4(pp + P_BK + 16 * (OB * half + j) + 4 * g);
-      stage_gemm_half<true>(st, xn, a, half, lane);
+      for (int b = 0; b < NB; ++b)
 #pragma unroll
-      for (int j = 0; j < OB; ++j) {
-        const int ob = OB * half + j;
-        *reinterpret_cast<half4_t*>(k_lds + (16 * tb + r16) * LD + 32 * (ob / 2) + 8 * g + 4 * (ob & 1)) =
-            to_half4(a[j]);
-      }
+        for (int j = 0; j < OB; ++j) a[b][j] = ld4(pp + P_BK + 16 * (OB * half + j) + 4 * g);
+      stage_gemm2<true>(st, xn, a, half, lane);
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int j = 0; j < OB; ++j) {
+          const int ob = OB * half + j;
+          *reinterpret_cast<half4_t*>(k_lds + (16 * tb[b] + r16) * LD + 32 * (ob / 2) + 8 * g + 4 * (ob & 1)) =
+              to_half4(a[b][j]);
+        }
     }
     // ---- V (own features) -> V^T in LDS -------------------------------------
     {
       const char* st = begin_group(g0 + 2);
-      float4_t a[OB];
+      float4_t a[NB][OB];
 #pragma unroll
       for (int j = 0; j < OB; ++j) {
         const float bv = pp[P_BV + 16 * (OB * half + j) + r16];
-        a[j] = float4_t{bv, bv, bv, bv};
-      }
-      stage_gemm_half<false>(st, xn, a, half, lane);
 #pragma unroll
-      for (int j = 0; j < OB; ++j)
-        *reinterpret_cast<half4_t*>(vt_lds + (16 * (OB * half + j) + r16) * LD + 16 * tb + 4 * g) = to_half4(a[j]);
+        for (int b = 0; b < NB; ++b) a[b][j] = float4_t{bv, bv, bv, bv};
+      }
+      stage_gemm2<false>(st, xn, a, half, lane);
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int j = 0; j < OB; ++j)
+          *reinterpret_cast<half4_t*>(vt_lds + (16 * (OB * half + j) + r16) * LD + 16 * tb[b] + 4 * g) =
+              to_half4(a[b][j]);
     }
     lds_barrier();  // K and V^T of every token block are in LDS
 
-    // ---- causal attention of the block's queries, own heads -----------------
-    // One specialisation per query block: with the key-block count known at
-    // compile time the heads' MFMA and softmax work forms one branch-free
-    // stretch the scheduler can interleave.
-    half8_t cop[KS];
+    // ---- causal attention of both blocks, own heads --------------------------
+    half8_t cop[NB][KS];
 #pragma unroll
-    for (int j = 0; j < OK; ++j) cop[OK * half + j] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
-    switch (tb) {
-      case 0: attend16<HD, HALF, 0, MASK>(k_lds, vt_lds, L.kval, qop, cop, g, r16); break;
-      case 1: attend16<HD, HALF, 1, MASK>(k_lds, vt_lds, L.kval, qop, cop, g, r16); break;
-      case 2: attend16<HD, HALF, 2, MASK>(k_lds, vt_lds, L.kval, qop, cop, g, r16); break;
-      case 3: attend16<HD, HALF, 3, MASK>(k_lds, vt_lds, L.kval, qop, cop, g, r16); break;
-      case 4: attend16<HD, HALF, 4, MASK>(k_lds, vt_lds, L.kval, qop, cop, g, r16); break;
-      case 5: attend16<HD, HALF, 5, MASK>(k_lds, vt_lds, L.kval, qop, cop, g, r16); break;
-      case 6: attend16<HD, HALF, 6, MASK>(k_lds, vt_lds, L.kval, qop, cop, g, r16); break;
-      default: attend16<HD, HALF, 7, MASK>(k_lds, vt_lds, L.kval, qop, cop, g, r16); break;
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int j = 0; j < OK; ++j) cop[b][OK * half + j] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+    switch (pair) {
+      case 0: attend_pair<HD, HALF, 0, MASK>(L, qop, cop, g, r16); break;
+      case 1: attend_pair<HD, HALF, 1, MASK>(L, qop, cop, g, r16); break;
+      case 2: attend_pair<HD, HALF, 2, MASK>(L, qop, cop, g, r16); break;
+      default: attend_pair<HD, HALF, 3, MASK>(L, qop, cop, g, r16); break;
     }
     lds_barrier();  // every wave is done with K and V^T: their areas take exchanges now
     {
-      half8_t own[OK];
+      half8_t own[NB][OK];
 #pragma unroll
-      for (int j = 0; j < OK; ++j) own[j] = cop[OK * half + j];
-      put_half(area_b, own, cop, tb, half, lane);
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int j = 0; j < OK; ++j) own[b][j] = cop[b][OK * half + j];
+      put_half2(area_b, own, cop, tb, half, lane);
     }
 
     // ---- output projection + residual (own features) ------------------------
     {
       const char* st = begin_group(g0 + 3);
-      get_partner(area_b, cop, tb, half, lane);
-      float4_t a[OB];
+      get_partner2(area_b, cop, tb, half, lane);
+      float4_t a[NB][OB];
 #pragma unroll
-      for (int j = 0; j < OB; ++j) a[j] = ld4(pp + P_BO + 16 * (OB * half + j) + 4 * g);
-      stage_gemm_half<true>(st, cop, a, half, lane);
+      for (int b = 0; b < NB; ++b)
 #pragma unroll
-      for (int j = 0; j < OB; ++j) res[j] += a[j];
+        for (int j = 0; j < OB; ++j) a[b][j] = ld4(pp + P_BO + 16 * (OB * half + j) + 4 * g);
+      stage_gemm2<true>(st, cop, a, half, lane);
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int j = 0; j < OB; ++j) res[b][j] += a[b][j];
     }
 
     // ---- LN2, FFN -------------------------------------------------------------
     {
-      half8_t own[OK];
-      split_layer_norm(res, pp + P_G2, pp + P_BE2, (affine_mask >> min(2 * layer + 1, 63)) & 1, xstat[1], wave, lane, half,
-                       g, own);
-      put_half(area_a, own, xn, tb, half, lane);
+      half8_t own[NB][OK];
+      split_layer_norm2(res, pp + P_G2, pp + P_BE2, (affine_mask >> min(2 * layer + 1, 63)) & 1, xstat[1], wave,
+                        lane, half, g, own);
+      put_half2(area_a, own, xn, tb, half, lane);
     }
-    half8_t hf[KS];
+    half8_t hf[NB][KS];
     {
       const char* st = begin_group(g0 + 4);
-      get_partner(area_a, xn, tb, half, lane);
-      float4_t a[OB];
+      get_partner2(area_a, xn, tb, half, lane);
+      float4_t a[NB][OB];
 #pragma unroll
-      for (int j = 0; j < OB; ++j) a[j] = ld4(pp + P_B1 + 16 * (OB * half + j) + 4 * g);
-      stage_gemm_half<true>(st, xn, a, half, lane);
-      half8_t own[OK];
+      for (int b = 0; b < NB; ++b)
 #pragma unroll
-      for (int j = 0; j < OB; ++j)
+        for (int j = 0; j < OB; ++j) a[b][j] = ld4(pp + P_B1 + 16 * (OB * half + j) + 4 * g);
+      stage_gemm2<true>(st, xn, a, half, lane);
+      half8_t own[NB][OK];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) own[j / 2][(j & 1) * 4 + i] = (half_t)gelu_erf(a[j][i]);
-      put_half(area_b, own, hf, tb, half, lane);
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int j = 0; j < OB; ++j)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) own[b][j / 2][(j & 1) * 4 + i] = (half_t)gelu_erf(a[b][j][i]);
+      put_half2(area_b, own, hf, tb, half, lane);
     }
     {
       const char* st = begin_group(g0 + 5);
-      get_partner(area_b, hf, tb, half, lane);
-      float4_t a[OB];
+      get_partner2(area_b, hf, tb, half, lane);
+      float4_t a[NB][OB];
 #pragma unroll
-      for (int j = 0; j < OB; ++j) a[j] = ld4(pp + P_B2 + 16 * (OB * half + j) + 4 * g);
-      stage_gemm_half<true>(st, hf, a, half, lane);
+      for (int b = 0; b < NB; ++b)
 #pragma unroll
-      for (int j = 0; j < OB; ++j) res[j] += a[j];
+        for (int j = 0; j < OB; ++j) a[b][j] = ld4(pp + P_B2 + 16 * (OB * half + j) + 4 * g);
+      stage_gemm2<true>(st, hf, a, half, lane);
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int j = 0; j < OB; ++j) res[b][j] += a[b][j];
     }
   }
 
@@ -840,32 +900,33 @@ __device__ __forceinline__ void stack16_body(Lds& L, const float* __restrict__ x
   drain_and_barrier();
   const float* gf = prm[layers & 1];
   const float* bf = gf + D;
-  float mean, rstd;
-  split_row_stats(res, xstat[0], wave, lane, mean, rstd);
-  // The output address is rebuilt from an opaque copy of the lane id, so the
-  // compiler does not keep the input-side token offset live across the layer
-  // loop (at 128 VGPRs it would spill it).
+  float mean[NB], rstd[NB];
+  split_row_stats2(res, xstat[0], wave, lane, mean, rstd);
   int lane_o = lane;
   asm volatile("" : "+v"(lane_o));
-  const int tok_o = 16 * tb + lane_o % 16, g_o = lane_o / 16;
-  if (tok_o < S) {
-    float* yrow = y + (seq * S + tok_o) * D;
-    // Padded tokens leave as zero rows (torch_transformer_benchmark.py:1146-1147).
-    const bool zero = MASK != 0 && L.kval[tok_o] == 0;
+  const int g_o = lane_o / 16;
 #pragma unroll
-    for (int j = 0; j < OB; ++j) {
-      const int f0 = 16 * (OB * half + j) + 4 * g_o;
-      const float4_t gg = ld4(gf + f0), bb = ld4(bf + f0);
-      float4_t o;
+  for (int b = 0; b < NB; ++b) {
+    const int tok_o = 16 * tb[b] + lane_o % 16;
+    if (tok_o < S) {
+      float* yrow = y + (seq * S + tok_o) * D;
+      // Padded tokens leave as zero rows (torch_transformer_benchmark.py:1146-1147).
+      const bool zero = MASK != 0 && L.kval[tok_o] == 0;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = zero ? 0.f : (res[j][i] - mean) * rstd * gg[i] + bb[i];
-      *reinterpret_cast<float4_t*>(yrow + f0) = o;  // (final LN: always affine, once per token)
+      for (int j = 0; j < OB; ++j) {
+        const int f0 = 16 * (OB * half + j) + 4 * g_o;
+        const float4_t gg = ld4(gf + f0), bb = ld4(bf + f0);
+        float4_t o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = zero ? 0.f : (res[b][j][i] - mean[b]) * rstd[b] * gg[i] + bb[i];
+        *reinterpret_cast<float4_t*>(yrow + f0) = o;
+      }
     }
   }
 }
 
 template <int HD, int MASK>
-__global__ __launch_bounds__(64 * NW, 1) void fused_stack16_kernel(
+__global__ __launch_bounds__(64 * NW, 1) void fused_stack8x2_kernel(
     const float* __restrict__ x, float* __restrict__ y, const half_t* __restrict__ wpack,
     const float* __restrict__ ppack, int S, int layers, int64_t affine_mask,
     const uint8_t* __restrict__ token_valid) {
@@ -873,20 +934,18 @@ __global__ __launch_bounds__(64 * NW, 1) void fused_stack16_kernel(
   if constexpr (MASK != 0) {
     // Token t is valid iff t < S and its byte of token_valid ([B, S], NULL =
     // all) is nonzero.  Visible after the first barrier in the body.
-    const int t = threadIdx.x;
-    if (t < SMAX)
+    for (int t = threadIdx.x; t < SMAX; t += 64 * NW)
       lds.kval[t] = t < S && (token_valid == nullptr || token_valid[(int64_t)blockIdx.x * S + t] != 0) ? 1 : 0;
   }
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int wi = wave % 8;
-  const int tb = wi < 4 ? wi : 11 - wi;  // the four waves of a SIMD hold blocks b, 7-b (both halves)
-  if (wave < 8)
-    stack16_body<HD, 0, MASK>(lds, x, y, wpack, ppack, S, layers, affine_mask, wave, tb);
+  const int pair = wave % 4;  // waves w and w + 4 (the two halves of blocks pair, 7 - pair) share a SIMD
+  if (wave < 4)
+    stack8x2_body<HD, 0, MASK>(lds, x, y, wpack, ppack, S, layers, affine_mask, wave, pair);
   else
-    stack16_body<HD, 1, MASK>(lds, x, y, wpack, ppack, S, layers, affine_mask, wave, tb);
+    stack8x2_body<HD, 1, MASK>(lds, x, y, wpack, ppack, S, layers, affine_mask, wave, pair);
 }
 
-}  // namespace w16
+}  // namespace w8x2
 
 // Fragment-major FP16 packing of an nn.Linear weight [n, k] (FP32 source).
 // permuted: k index 32ks + 4(l/16) + (m&3) + 16(m>>2); natural: 32ks + 8(l/16) + m.
@@ -915,15 +974,15 @@ template <int HD>
 static hipError_t launch(const float* x, float* y, const half_t* w, const float* p, int64_t batch, int S,
                          int layers, int64_t affine_mask, const uint8_t* token_valid, int causal, hipStream_t s) {
   if constexpr (HD <= 64) {
-    const dim3 grid((unsigned)batch), block(64 * w16::NW);
+    const dim3 grid((unsigned)batch), block(64 * w8x2::NW);
     if (!causal)
-      hipLaunchKernelGGL((w16::fused_stack16_kernel<HD, 2>), grid, block, 0, s, x, y, w, p, S, layers, affine_mask,
+      hipLaunchKernelGGL((w8x2::fused_stack8x2_kernel<HD, 2>), grid, block, 0, s, x, y, w, p, S, layers, affine_mask,
                          token_valid);
     else if (token_valid != nullptr)
-      hipLaunchKernelGGL((w16::fused_stack16_kernel<HD, 1>), grid, block, 0, s, x, y, w, p, S, layers, affine_mask,
+      hipLaunchKernelGGL((w8x2::fused_stack8x2_kernel<HD, 1>), grid, block, 0, s, x, y, w, p, S, layers, affine_mask,
                          token_valid);
     else
-      hipLaunchKernelGGL((w16::fused_stack16_kernel<HD, 0>), grid, block, 0, s, x, y, w, p, S, layers, affine_mask,
+      hipLaunchKernelGGL((w8x2::fused_stack8x2_kernel<HD, 0>), grid, block, 0, s, x, y, w, p, S, layers, affine_mask,
                          token_valid);
   } else {
     hipLaunchKernelGGL((fused_stack_kernel<HD>), dim3((unsigned)batch), dim3(64 * NW), 0, s, x, y, w, p, S, layers);
