@@ -50,6 +50,8 @@ EXPORTED_SYMBOLS = (
     "xb_attention_kv_cache",
     "xb_pack_linear_fragments",
     "xb_fused_forward_d128",
+    "xb_fused_forward_d128_workspace_bytes",
+    "xb_fused_forward_d128_ws",
 )
 
 _vp = ctypes.c_void_p
@@ -80,6 +82,11 @@ _SIGNATURES = {
     ),
     "xb_pack_linear_fragments": (ctypes.c_int, [_vp, _vp, _i32, _i32, _i32, _f32, _vp]),
     "xb_fused_forward_d128": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i64, _vp, _i32, _vp]),
+    "xb_fused_forward_d128_workspace_bytes": (_i64, [_i64, _i32, _i32, _i32, _i32]),
+    "xb_fused_forward_d128_ws": (
+        ctypes.c_int,
+        [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i64, _vp, _i32, _vp, _i64, _vp],
+    ),
 }
 
 _LIB: Optional[ctypes.CDLL] = None

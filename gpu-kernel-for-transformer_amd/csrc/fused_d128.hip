@@ -580,16 +580,16 @@ using split::Lds;
 using split::lds_barrier;
 
 // a[b][j] += staged-matrix output block (OB*half + j) times the operands of block b.
-template <bool SWAP>
-__device__ __forceinline__ void stage_gemm2(const char* st, const half8_t (&act)[NB][KS], float4_t (&a)[NB][OB], int half,
-                                            int lane) {
+template <bool SWAP, int NBT>
+__device__ __forceinline__ void stage_gemm2(const char* st, const half8_t (&act)[NBT][KS], float4_t (&a)[NBT][OB],
+                                            int half, int lane) {
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
     half8_t f[OB];
 #pragma unroll
     for (int j = 0; j < OB; ++j) f[j] = sfrag(st, (OB * half + j) * KS + ks, lane);
 #pragma unroll
-    for (int b = 0; b < NB; ++b)
+    for (int b = 0; b < NBT; ++b)
 #pragma unroll
       for (int j = 0; j < OB; ++j)
         a[b][j] = SWAP ? mfma16x16x32(f[j], act[b][ks], a[b][j]) : mfma16x16x32(act[b][ks], f[j], a[b][j]);
@@ -600,11 +600,12 @@ __device__ __forceinline__ void stage_gemm2(const char* st, const half8_t (&act)
 // each wave's (mean, M2) over its 64 features meet in LDS and merge by Chan's
 // pairwise formula (equal counts: M2 = M2a + M2b + (ma - mb)^2 * 32); both
 // waves of a pair get bit-identical results (the merge is symmetric).
-__device__ __forceinline__ void split_row_stats2(const float4_t (&r)[NB][OB], float2* xs, int wave, int lane,
-                                                 float (&mean)[NB], float (&rstd)[NB]) {
-  float ma[NB], m2a[NB];
+template <int NBT>
+__device__ __forceinline__ void split_row_stats2(const float4_t (&r)[NBT][OB], float2* xs, int wave, int lane,
+                                                 float (&mean)[NBT], float (&rstd)[NBT]) {
+  float ma[NBT], m2a[NBT];
 #pragma unroll
-  for (int b = 0; b < NB; ++b) {
+  for (int b = 0; b < NBT; ++b) {
     float s = 0.f;
 #pragma unroll
     for (int j = 0; j < OB; ++j) s += (r[b][j][0] + r[b][j][1]) + (r[b][j][2] + r[b][j][3]);
@@ -620,12 +621,12 @@ __device__ __forceinline__ void split_row_stats2(const float4_t (&r)[NB][OB], fl
   asm volatile("" : "+v"(l));
   if (l < 16) {
 #pragma unroll
-    for (int b = 0; b < NB; ++b) xs[(wave * NB + b) * 16 + l] = make_float2(ma[b], m2a[b]);
+    for (int b = 0; b < NBT; ++b) xs[(wave * NBT + b) * 16 + l] = make_float2(ma[b], m2a[b]);
   }
   lds_barrier();
 #pragma unroll
-  for (int b = 0; b < NB; ++b) {
-    const float2 pb = xs[((wave ^ 4) * NB + b) * 16 + l % 16];
+  for (int b = 0; b < NBT; ++b) {
+    const float2 pb = xs[((wave ^ 4) * NBT + b) * 16 + l % 16];
     const float d = pb.x - ma[b];
     mean[b] = 0.5f * (ma[b] + pb.x);
     rstd[b] = __builtin_amdgcn_rsqf(((m2a[b] + pb.y) + d * d * 32.f) * (1.0f / D) + 1e-5f);
@@ -633,13 +634,14 @@ __device__ __forceinline__ void split_row_stats2(const float4_t (&r)[NB][OB], fl
 }
 
 // LayerNorm of the wave's half of both blocks -> their own k-steps of operand.
-__device__ __forceinline__ void split_layer_norm2(const float4_t (&res)[NB][OB], const float* gamma, const float* beta,
+template <int NBT>
+__device__ __forceinline__ void split_layer_norm2(const float4_t (&res)[NBT][OB], const float* gamma, const float* beta,
                                                   bool affine, float2* xs, int wave, int lane, int half, int g,
-                                                  half8_t (&own)[NB][OK]) {
-  float mean[NB], rstd[NB];
+                                                  half8_t (&own)[NBT][OK]) {
+  float mean[NBT], rstd[NBT];
   split_row_stats2(res, xs, wave, lane, mean, rstd);
 #pragma unroll
-  for (int b = 0; b < NB; ++b) {
+  for (int b = 0; b < NBT; ++b) {
     const float shift = -mean[b] * rstd[b];
 #pragma unroll
     for (int j = 0; j < OK; ++j) {
@@ -666,10 +668,11 @@ __device__ __forceinline__ void split_layer_norm2(const float4_t (&res)[NB][OB],
 }
 
 // Own k-steps of both blocks into their exchange slots and into `full`.
-__device__ __forceinline__ void put_half2(char* area, const half8_t (&own)[NB][OK], half8_t (&full)[NB][KS],
-                                          const int (&tb)[NB], int half, int lane) {
+template <int NBT>
+__device__ __forceinline__ void put_half2(char* area, const half8_t (&own)[NBT][OK], half8_t (&full)[NBT][KS],
+                                          const int (&tb)[NBT], int half, int lane) {
 #pragma unroll
-  for (int b = 0; b < NB; ++b)
+  for (int b = 0; b < NBT; ++b)
 #pragma unroll
     for (int j = 0; j < OK; ++j) {
       *xslot(area, tb[b], half, j, lane) = own[b][j];
@@ -677,10 +680,11 @@ __device__ __forceinline__ void put_half2(char* area, const half8_t (&own)[NB][O
     }
 }
 // After a barrier that follows the partner's put_half2.
-__device__ __forceinline__ void get_partner2(char* area, half8_t (&full)[NB][KS], const int (&tb)[NB], int half,
+template <int NBT>
+__device__ __forceinline__ void get_partner2(char* area, half8_t (&full)[NBT][KS], const int (&tb)[NBT], int half,
                                              int lane) {
 #pragma unroll
-  for (int b = 0; b < NB; ++b)
+  for (int b = 0; b < NBT; ++b)
 #pragma unroll
     for (int j = 0; j < OK; ++j) full[b][OK * (half ^ 1) + j] = *xslot(area, tb[b], half ^ 1, j, lane);
 }
@@ -693,10 +697,72 @@ __device__ __forceinline__ void attend_pair(const Lds& L, const half8_t (&qop)[N
   split::attend16<HD, HALF, 7 - P, MASK>(L.k, L.vt, L.kval, qop[1], cop[1], g, r16);
 }
 
-template <int HD, int HALF, int MASK>
+// K/V exchange of the split form.  Per (sequence, layer) a 32 KB slot: K rows
+// of tokens 0..63 ([64][128] halves) then their V^T columns ([128][64]), and
+// an int flag; part 0 stores the slot and raises the flag (release, agent
+// scope), part 1 waits for it (acquire), copies the slot into its LDS and
+// lowers the flag again, so every flag is back to zero when the kernel ends
+// (graph replays reuse the workspace as it is).  Part 1 only waits on part 0, which has the
+// lower block index and so was dispatched first: the wait ends.  It is still
+// bounded; running out counts an error in `errors` and goes on.
+struct SplitExchange {
+  half_t* kv;      // [batch][layers][2][64 * 128]
+  int* flags;      // [batch][layers]
+  int* errors;     // one counter
+  int layers;
+};
+constexpr int kExchangeSpins = 1 << 20;
+
+__device__ __forceinline__ void publish_kv(const Lds& L, const SplitExchange& ex, int64_t seq, int layer) {
+  half_t* slot = ex.kv + (seq * ex.layers + layer) * (2 * 64 * 128);
+  const int t = threadIdx.x;  // 512 threads, two 16-byte chunks of K and two of V^T each
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int e = 2 * t + i;  // 1024 chunks per region
+    *reinterpret_cast<half8_t*>(slot + 8 * e) = *reinterpret_cast<const half8_t*>(L.k + (e / 16) * LD + 8 * (e % 16));
+    *reinterpret_cast<half8_t*>(slot + 64 * 128 + 8 * e) =
+        *reinterpret_cast<const half8_t*>(L.vt + (e / 8) * LD + 8 * (e % 8));
+  }
+  __syncthreads();  // every thread's stores are done
+  if (t == 0) __hip_atomic_store(ex.flags + seq * ex.layers + layer, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void fetch_kv(Lds& L, const SplitExchange& ex, int64_t seq, int layer) {
+  const half_t* slot = ex.kv + (seq * ex.layers + layer) * (2 * 64 * 128);
+  int* flag = ex.flags + seq * ex.layers + layer;
+  const int t = threadIdx.x;
+  if (t == 0) {
+    int spins = 0;
+    while (__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) == 0) {
+      __builtin_amdgcn_s_sleep(1);
+      if (++spins > kExchangeSpins) {
+        atomicAdd(ex.errors, 1);
+        break;
+      }
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int e = 2 * t + i;
+    *reinterpret_cast<half8_t*>(L.k + (e / 16) * LD + 8 * (e % 16)) = *reinterpret_cast<const half8_t*>(slot + 8 * e);
+    *reinterpret_cast<half8_t*>(L.vt + (e / 8) * LD + 8 * (e % 8)) =
+        *reinterpret_cast<const half8_t*>(slot + 64 * 128 + 8 * e);
+  }
+  __syncthreads();  // the fetched rows are in LDS (and the slot is read)
+  if (t == 0) __hip_atomic_store(flag, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// NBT = 2: the pair form above (blocks pair, 7 - pair per wave, one workgroup
+// per sequence).  NBT = 1 with SPLIT: two workgroups per sequence, `part` 0
+// holding blocks 0-3 and part 1 blocks 4-7, one block (pair + 4 part) and one
+// feature half per wave; part 0 publishes each layer's K and V^T of tokens
+// 0..63 to `ex` and part 1 fetches them before its attention.
+template <int HD, int HALF, int MASK, int NBT, bool SPLIT>
 __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ x, float* __restrict__ y,
                                               const half_t* __restrict__ wpack, const float* __restrict__ ppack,
-                                              int S, int layers, int64_t affine_mask, int wave, int pair) {
+                                              int S, int layers, int64_t affine_mask, int wave, int pair,
+                                              int64_t seq, int part, const SplitExchange& ex) {
   constexpr int H = D / HD;
   static_assert(H >= 2, "heads split between the two halves");
   constexpr int half = HALF;
@@ -710,10 +776,15 @@ __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ 
 
   const int lane = threadIdx.x % kWave;
   const int g = lane / 16, r16 = lane % 16;
-  const int64_t seq = blockIdx.x;
   const float* xs = x + seq * S * D;
   const int groups = layers * MATS;
-  const int tb[NB] = {pair, 7 - pair};
+  int tb[NBT];
+  if constexpr (NBT == 2) {
+    tb[0] = pair;
+    tb[1] = 7 - pair;
+  } else {
+    tb[0] = 4 * part + pair;
+  }
 
   auto issue_group = [&](int gi) {
     const int layer = gi / MATS, m = gi % MATS;
@@ -739,9 +810,9 @@ __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ 
   };
 
   // Residual stream, own half of both blocks: res[b][j][i] = x[16 tb[b] + r16][16 (OB half + j) + 4 g + i].
-  float4_t res[NB][OB];
+  float4_t res[NBT][OB];
 #pragma unroll
-  for (int b = 0; b < NB; ++b) {
+  for (int b = 0; b < NBT; ++b) {
     const int tok = 16 * tb[b] + r16;
 #pragma unroll
     for (int j = 0; j < OB; ++j)
@@ -754,41 +825,41 @@ __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ 
   for (int layer = 0; layer < layers; ++layer) {
     const float* pp = prm[layer & 1];
     const int g0 = layer * MATS;
-    half8_t xn[NB][KS];
+    half8_t xn[NBT][KS];
     {
-      half8_t own[NB][OK];
+      half8_t own[NBT][OK];
       split_layer_norm2(res, pp + P_G1, pp + P_BE1, (affine_mask >> min(2 * layer, 63)) & 1, xstat[0], wave, lane,
                         half, g, own);
       put_half2(area_a, own, xn, tb, half, lane);
     }
 
     // ---- Q (own heads), kept in registers --------------------------------
-    half8_t qop[NB][OK];
+    half8_t qop[NBT][OK];
     {
       const char* st = begin_group(g0 + 0);
       get_partner2(area_a, xn, tb, half, lane);
-      float4_t qc[NB][OB];
+      float4_t qc[NBT][OB];
 #pragma unroll
-      for (int b = 0; b < NB; ++b)
+      for (int b = 0; b < NBT; ++b)
 #pragma unroll
         for (int j = 0; j < OB; ++j) qc[b][j] = ld4(pp + P_BQ + 16 * (OB * half + j) + 4 * g);
       stage_gemm2<true>(st, xn, qc, half, lane);
 #pragma unroll
-      for (int b = 0; b < NB; ++b)
+      for (int b = 0; b < NBT; ++b)
 #pragma unroll
         for (int j = 0; j < OK; ++j) qop[b][j] = to_operand(qc[b][2 * j], qc[b][2 * j + 1]);
     }
     // ---- K (own features) -> LDS, permuted per k-step ----------------------
     {
       const char* st = begin_group(g0 + 1);
-      float4_t a[NB][OB];
+      float4_t a[NBT][OB];
 #pragma unroll
-      for (int b = 0; b < NB; ++b)
+      for (int b = 0; b < NBT; ++b)
 #pragma unroll
         for (int j = 0; j < OB; ++j) a[b][j] = ld4(pp + P_BK + 16 * (OB * half + j) + 4 * g);
       stage_gemm2<true>(st, xn, a, half, lane);
 #pragma unroll
-      for (int b = 0; b < NB; ++b)
+      for (int b = 0; b < NBT; ++b)
 #pragma unroll
         for (int j = 0; j < OB; ++j) {
           const int ob = OB * half + j;
@@ -799,40 +870,59 @@ __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ 
     // ---- V (own features) -> V^T in LDS -------------------------------------
     {
       const char* st = begin_group(g0 + 2);
-      float4_t a[NB][OB];
+      float4_t a[NBT][OB];
 #pragma unroll
       for (int j = 0; j < OB; ++j) {
         const float bv = pp[P_BV + 16 * (OB * half + j) + r16];
 #pragma unroll
-        for (int b = 0; b < NB; ++b) a[b][j] = float4_t{bv, bv, bv, bv};
+        for (int b = 0; b < NBT; ++b) a[b][j] = float4_t{bv, bv, bv, bv};
       }
       stage_gemm2<false>(st, xn, a, half, lane);
 #pragma unroll
-      for (int b = 0; b < NB; ++b)
+      for (int b = 0; b < NBT; ++b)
 #pragma unroll
         for (int j = 0; j < OB; ++j)
           *reinterpret_cast<half4_t*>(vt_lds + (16 * (OB * half + j) + r16) * LD + 16 * tb[b] + 4 * g) =
               to_half4(a[b][j]);
     }
     lds_barrier();  // K and V^T of every token block are in LDS
+    if constexpr (SPLIT) {
+      if (part == 0)
+        publish_kv(L, ex, seq, layer);
+      else
+        fetch_kv(L, ex, seq, layer);
+    }
 
     // ---- causal attention of both blocks, own heads --------------------------
-    half8_t cop[NB][KS];
+    half8_t cop[NBT][KS];
 #pragma unroll
-    for (int b = 0; b < NB; ++b)
+    for (int b = 0; b < NBT; ++b)
 #pragma unroll
       for (int j = 0; j < OK; ++j) cop[b][OK * half + j] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
-    switch (pair) {
-      case 0: attend_pair<HD, HALF, 0, MASK>(L, qop, cop, g, r16); break;
-      case 1: attend_pair<HD, HALF, 1, MASK>(L, qop, cop, g, r16); break;
-      case 2: attend_pair<HD, HALF, 2, MASK>(L, qop, cop, g, r16); break;
-      default: attend_pair<HD, HALF, 3, MASK>(L, qop, cop, g, r16); break;
+    if constexpr (NBT == 2) {
+      switch (pair) {
+        case 0: attend_pair<HD, HALF, 0, MASK>(L, qop, cop, g, r16); break;
+        case 1: attend_pair<HD, HALF, 1, MASK>(L, qop, cop, g, r16); break;
+        case 2: attend_pair<HD, HALF, 2, MASK>(L, qop, cop, g, r16); break;
+        default: attend_pair<HD, HALF, 3, MASK>(L, qop, cop, g, r16); break;
+      }
+    } else {
+      switch (tb[0]) {
+        case 0: split::attend16<HD, HALF, 0, MASK>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16); break;
+        case 1: split::attend16<HD, HALF, 1, MASK>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16); break;
+        case 2: split::attend16<HD, HALF, 2, MASK>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16); break;
+        case 3: split::attend16<HD, HALF, 3, MASK>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16); break;
+        case 4: split::attend16<HD, HALF, 4, MASK>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16); break;
+        case 5: split::attend16<HD, HALF, 5, MASK>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16); break;
+        case 6: split::attend16<HD, HALF, 6, MASK>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16); break;
+        default: split::attend16<HD, HALF, 7, MASK>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16); break;
+      }
     }
     lds_barrier();  // every wave is done with K and V^T: their areas take exchanges now
     {
-      half8_t own[NB][OK];
+      half8_t own[NBT][OK];
 #pragma unroll
-      for (int b = 0; b < NB; ++b)
+      for (int b = 0; b < NBT; ++b)
 #pragma unroll
         for (int j = 0; j < OK; ++j) own[b][j] = cop[b][OK * half + j];
       put_half2(area_b, own, cop, tb, half, lane);
@@ -842,38 +932,38 @@ __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ 
     {
       const char* st = begin_group(g0 + 3);
       get_partner2(area_b, cop, tb, half, lane);
-      float4_t a[NB][OB];
+      float4_t a[NBT][OB];
 #pragma unroll
-      for (int b = 0; b < NB; ++b)
+      for (int b = 0; b < NBT; ++b)
 #pragma unroll
         for (int j = 0; j < OB; ++j) a[b][j] = ld4(pp + P_BO + 16 * (OB * half + j) + 4 * g);
       stage_gemm2<true>(st, cop, a, half, lane);
 #pragma unroll
-      for (int b = 0; b < NB; ++b)
+      for (int b = 0; b < NBT; ++b)
 #pragma unroll
         for (int j = 0; j < OB; ++j) res[b][j] += a[b][j];
     }
 
     // ---- LN2, FFN -------------------------------------------------------------
     {
-      half8_t own[NB][OK];
+      half8_t own[NBT][OK];
       split_layer_norm2(res, pp + P_G2, pp + P_BE2, (affine_mask >> min(2 * layer + 1, 63)) & 1, xstat[1], wave,
                         lane, half, g, own);
       put_half2(area_a, own, xn, tb, half, lane);
     }
-    half8_t hf[NB][KS];
+    half8_t hf[NBT][KS];
     {
       const char* st = begin_group(g0 + 4);
       get_partner2(area_a, xn, tb, half, lane);
-      float4_t a[NB][OB];
+      float4_t a[NBT][OB];
 #pragma unroll
-      for (int b = 0; b < NB; ++b)
+      for (int b = 0; b < NBT; ++b)
 #pragma unroll
         for (int j = 0; j < OB; ++j) a[b][j] = ld4(pp + P_B1 + 16 * (OB * half + j) + 4 * g);
       stage_gemm2<true>(st, xn, a, half, lane);
-      half8_t own[NB][OK];
+      half8_t own[NBT][OK];
 #pragma unroll
-      for (int b = 0; b < NB; ++b)
+      for (int b = 0; b < NBT; ++b)
 #pragma unroll
         for (int j = 0; j < OB; ++j)
 #pragma unroll
@@ -883,14 +973,14 @@ __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ 
     {
       const char* st = begin_group(g0 + 5);
       get_partner2(area_b, hf, tb, half, lane);
-      float4_t a[NB][OB];
+      float4_t a[NBT][OB];
 #pragma unroll
-      for (int b = 0; b < NB; ++b)
+      for (int b = 0; b < NBT; ++b)
 #pragma unroll
         for (int j = 0; j < OB; ++j) a[b][j] = ld4(pp + P_B2 + 16 * (OB * half + j) + 4 * g);
       stage_gemm2<true>(st, hf, a, half, lane);
 #pragma unroll
-      for (int b = 0; b < NB; ++b)
+      for (int b = 0; b < NBT; ++b)
 #pragma unroll
         for (int j = 0; j < OB; ++j) res[b][j] += a[b][j];
     }
@@ -900,13 +990,13 @@ __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ 
   drain_and_barrier();
   const float* gf = prm[layers & 1];
   const float* bf = gf + D;
-  float mean[NB], rstd[NB];
+  float mean[NBT], rstd[NBT];
   split_row_stats2(res, xstat[0], wave, lane, mean, rstd);
   int lane_o = lane;
   asm volatile("" : "+v"(lane_o));
   const int g_o = lane_o / 16;
 #pragma unroll
-  for (int b = 0; b < NB; ++b) {
+  for (int b = 0; b < NBT; ++b) {
     const int tok_o = 16 * tb[b] + lane_o % 16;
     if (tok_o < S) {
       float* yrow = y + (seq * S + tok_o) * D;
@@ -939,10 +1029,35 @@ __global__ __launch_bounds__(64 * NW, 1) void fused_stack8x2_kernel(
   }
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int pair = wave % 4;  // waves w and w + 4 (the two halves of blocks pair, 7 - pair) share a SIMD
+  const SplitExchange none{nullptr, nullptr, nullptr, 0};
   if (wave < 4)
-    stack8x2_body<HD, 0, MASK>(lds, x, y, wpack, ppack, S, layers, affine_mask, wave, pair);
+    stack8x2_body<HD, 0, MASK, 2, false>(lds, x, y, wpack, ppack, S, layers, affine_mask, wave, pair, blockIdx.x, 0, none);
   else
-    stack8x2_body<HD, 1, MASK>(lds, x, y, wpack, ppack, S, layers, affine_mask, wave, pair);
+    stack8x2_body<HD, 1, MASK, 2, false>(lds, x, y, wpack, ppack, S, layers, affine_mask, wave, pair, blockIdx.x, 0, none);
+}
+
+// Split form (causal only, MASK 0 or 1): block b < batch is part 0 of
+// sequence b, block batch + b part 1 of it (when batch % 8 == 0 the two share
+// an XCD: blocks are dealt to the eight XCDs round-robin).
+template <int HD, int MASK>
+__global__ __launch_bounds__(64 * NW, 1) void fused_split_kernel(
+    const float* __restrict__ x, float* __restrict__ y, const half_t* __restrict__ wpack,
+    const float* __restrict__ ppack, int S, int layers, int64_t affine_mask,
+    const uint8_t* __restrict__ token_valid, int batch, SplitExchange ex) {
+  static_assert(MASK != 2, "part 0 would need part 1's keys");
+  __shared__ Lds lds;
+  const int part = blockIdx.x >= (unsigned)batch ? 1 : 0;
+  const int64_t seq = blockIdx.x - part * batch;
+  if constexpr (MASK != 0) {
+    for (int t = threadIdx.x; t < SMAX; t += 64 * NW)
+      lds.kval[t] = t < S && (token_valid == nullptr || token_valid[seq * S + t] != 0) ? 1 : 0;
+  }
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int pair = wave % 4;  // block 4 part + pair; waves w and w + 4 (its two halves) share a SIMD
+  if (wave < 4)
+    stack8x2_body<HD, 0, MASK, 1, true>(lds, x, y, wpack, ppack, S, layers, affine_mask, wave, pair, seq, part, ex);
+  else
+    stack8x2_body<HD, 1, MASK, 1, true>(lds, x, y, wpack, ppack, S, layers, affine_mask, wave, pair, seq, part, ex);
 }
 
 }  // namespace w8x2
@@ -970,10 +1085,40 @@ __global__ void pack_fragments_kernel(const float* __restrict__ w, half_t* __res
   out[idx] = (half_t)v;
 }
 
+// The split form (two workgroups per sequence) needs causal attention and
+// tokens in both halves.  Its time grows with the batch even below 256
+// workgroups (measured at S = 128, 4 layers: head_dim 32 gains 11% at B = 64,
+// 6% at B = 80, nothing at B = 96; head_dim 8 gains 16% at B = 64 and loses
+// at B = 128), so it stops at 80 sequences.
+constexpr int64_t kSplitMaxBatch = 80;
+static bool use_split(int64_t batch, int S, int hd, int causal) {
+  return hd <= 64 && causal && S > 64 && batch <= kSplitMaxBatch;
+}
+static int64_t split_workspace_bytes(int64_t batch, int layers) {
+  // K/V slots, then one flag per slot, then the timeout counter (the last 4 bytes).
+  return batch * layers * (2 * 64 * 128 * (int64_t)sizeof(half_t) + (int64_t)sizeof(int)) + (int64_t)sizeof(int);
+}
+
 template <int HD>
 static hipError_t launch(const float* x, float* y, const half_t* w, const float* p, int64_t batch, int S,
-                         int layers, int64_t affine_mask, const uint8_t* token_valid, int causal, hipStream_t s) {
+                         int layers, int64_t affine_mask, const uint8_t* token_valid, int causal, void* workspace,
+                         hipStream_t s) {
   if constexpr (HD <= 64) {
+    if (workspace != nullptr) {  // the caller checked use_split and the workspace size
+      char* ws = static_cast<char*>(workspace);
+      const int64_t kv_bytes = batch * layers * 2 * 64 * 128 * (int64_t)sizeof(half_t);
+      const w8x2::SplitExchange ex{reinterpret_cast<half_t*>(ws), reinterpret_cast<int*>(ws + kv_bytes),
+                                   reinterpret_cast<int*>(ws + kv_bytes + batch * layers * (int64_t)sizeof(int)),
+                                   layers};
+      const dim3 grid((unsigned)(2 * batch)), block(64 * w8x2::NW);
+      if (token_valid != nullptr)
+        hipLaunchKernelGGL((w8x2::fused_split_kernel<HD, 1>), grid, block, 0, s, x, y, w, p, S, layers, affine_mask,
+                           token_valid, (int)batch, ex);
+      else
+        hipLaunchKernelGGL((w8x2::fused_split_kernel<HD, 0>), grid, block, 0, s, x, y, w, p, S, layers, affine_mask,
+                           token_valid, (int)batch, ex);
+      return hipGetLastError();
+    }
     const dim3 grid((unsigned)batch), block(64 * w8x2::NW);
     if (!causal)
       hipLaunchKernelGGL((w8x2::fused_stack8x2_kernel<HD, 2>), grid, block, 0, s, x, y, w, p, S, layers, affine_mask,
@@ -1009,10 +1154,10 @@ extern "C" int xb_pack_linear_fragments(const float* w, void* out, int32_t n, in
   return (int)hipGetLastError();
 }
 
-extern "C" int xb_fused_forward_d128(const float* x, float* y, const void* wpack, const float* ppack,
-                                     int64_t batch, int32_t seq_len, int32_t heads, int32_t ffn_dim,
-                                     int32_t layers, int64_t affine_mask, const uint8_t* token_valid,
-                                     int32_t causal, void* stream) {
+static int fused_forward(const float* x, float* y, const void* wpack, const float* ppack, int64_t batch,
+                         int32_t seq_len, int32_t heads, int32_t ffn_dim, int32_t layers, int64_t affine_mask,
+                         const uint8_t* token_valid, int32_t causal, void* workspace, int64_t workspace_bytes,
+                         void* stream) {
   if (batch < 0 || seq_len <= 0 || heads <= 0 || ffn_dim <= 0 || layers <= 0) return XB_ERR_BAD_SIZE;
   if (batch > 0x7fffffffLL) return XB_ERR_BAD_SIZE;
   if (seq_len > fused::SMAX || fused::D % heads != 0) return XB_ERR_UNSUPPORTED_SHAPE;
@@ -1024,15 +1169,43 @@ extern "C" int xb_fused_forward_d128(const float* x, float* y, const void* wpack
   if (batch == 0) return XB_OK;
   if (!x || !y || !wpack || !ppack) return XB_ERR_NULL_POINTER;
   if (((uintptr_t)x | (uintptr_t)y | (uintptr_t)wpack | (uintptr_t)ppack) & 15u) return XB_ERR_MISALIGNED;
+  void* split_ws = nullptr;
+  if (workspace != nullptr && fused::use_split(batch, seq_len, hd, causal)) {
+    if (workspace_bytes < fused::split_workspace_bytes(batch, layers)) return XB_ERR_WORKSPACE;
+    if (((uintptr_t)workspace) & 15u) return XB_ERR_MISALIGNED;
+    split_ws = workspace;
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   const half_t* w = static_cast<const half_t*>(wpack);
   hipError_t e;
   switch (hd) {
-    case 8: e = fused::launch<8>(x, y, w, ppack, batch, seq_len, layers, affine_mask, token_valid, causal, s); break;
-    case 16: e = fused::launch<16>(x, y, w, ppack, batch, seq_len, layers, affine_mask, token_valid, causal, s); break;
-    case 32: e = fused::launch<32>(x, y, w, ppack, batch, seq_len, layers, affine_mask, token_valid, causal, s); break;
-    case 64: e = fused::launch<64>(x, y, w, ppack, batch, seq_len, layers, affine_mask, token_valid, causal, s); break;
-    default: e = fused::launch<128>(x, y, w, ppack, batch, seq_len, layers, affine_mask, token_valid, causal, s); break;
+    case 8: e = fused::launch<8>(x, y, w, ppack, batch, seq_len, layers, affine_mask, token_valid, causal, split_ws, s); break;
+    case 16: e = fused::launch<16>(x, y, w, ppack, batch, seq_len, layers, affine_mask, token_valid, causal, split_ws, s); break;
+    case 32: e = fused::launch<32>(x, y, w, ppack, batch, seq_len, layers, affine_mask, token_valid, causal, split_ws, s); break;
+    case 64: e = fused::launch<64>(x, y, w, ppack, batch, seq_len, layers, affine_mask, token_valid, causal, split_ws, s); break;
+    default: e = fused::launch<128>(x, y, w, ppack, batch, seq_len, layers, affine_mask, token_valid, causal, nullptr, s); break;
   }
   return (int)e;
+}
+
+extern "C" int xb_fused_forward_d128(const float* x, float* y, const void* wpack, const float* ppack,
+                                     int64_t batch, int32_t seq_len, int32_t heads, int32_t ffn_dim,
+                                     int32_t layers, int64_t affine_mask, const uint8_t* token_valid,
+                                     int32_t causal, void* stream) {
+  return fused_forward(x, y, wpack, ppack, batch, seq_len, heads, ffn_dim, layers, affine_mask, token_valid, causal,
+                       nullptr, 0, stream);
+}
+
+extern "C" int64_t xb_fused_forward_d128_workspace_bytes(int64_t batch, int32_t seq_len, int32_t heads,
+                                                         int32_t layers, int32_t causal) {
+  if (batch <= 0 || seq_len <= 0 || heads <= 0 || layers <= 0 || fused::D % heads != 0) return 0;
+  return fused::use_split(batch, seq_len, fused::D / heads, causal) ? fused::split_workspace_bytes(batch, layers) : 0;
+}
+
+extern "C" int xb_fused_forward_d128_ws(const float* x, float* y, const void* wpack, const float* ppack,
+                                        int64_t batch, int32_t seq_len, int32_t heads, int32_t ffn_dim,
+                                        int32_t layers, int64_t affine_mask, const uint8_t* token_valid,
+                                        int32_t causal, void* workspace, int64_t workspace_bytes, void* stream) {
+  return fused_forward(x, y, wpack, ppack, batch, seq_len, heads, ffn_dim, layers, affine_mask, token_valid, causal,
+                       workspace, workspace_bytes, stream);
 }

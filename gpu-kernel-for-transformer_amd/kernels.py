@@ -420,6 +420,7 @@ def fused_forward_d128(
     affine_mask: int = -1,
     token_valid: Optional[torch.Tensor] = None,
     causal: bool = True,
+    split: bool = True,
 ) -> torch.Tensor:
     """Whole-stack forward for d_model 128 / seq_len <= 128 (see xb_fused_forward_d128).
 
@@ -428,6 +429,9 @@ def fused_forward_d128(
     2l / 2l+1 set = apply layer l's norm1 / norm2 gamma and beta (-1: all).
     token_valid ([B, S] bool/uint8) and causal=False give the padding and
     non-causal semantics of `attention` (padded rows come out zero).
+    split=True lets a small causal batch run two workgroups per sequence
+    (xb_fused_forward_d128_ws) with a zero-filled workspace cached per device
+    and size; the results are the same bit for bit.
     """
     _require_device(x, "fused_forward_d128")
     if x.ndim != 3 or x.shape[-1] != 128 or x.dtype != torch.float32 or not x.is_contiguous():
@@ -436,11 +440,52 @@ def fused_forward_d128(
     if out is None:
         out = torch.empty_like(x)
     valid = None if token_valid is None else _byte_mask(token_valid, batch * seq_len, x.device, "token_valid")
+    ws = fused_split_workspace(x.device, batch, seq_len, num_heads, num_layers, causal) if split else None
+    ws_bytes = 0 if ws is None else ws.numel()
     check(
-        _launch("fused_forward_d128", lambda: lib().xb_fused_forward_d128(
+        _launch("fused_forward_d128_split" if ws is not None else "fused_forward_d128",
+                lambda: lib().xb_fused_forward_d128_ws(
             x.data_ptr(), out.data_ptr(), wpack.data_ptr(), ppack.data_ptr(), batch, seq_len,
             num_heads, ffn_dim, num_layers, int(affine_mask), _ptr(valid), int(bool(causal)),
-            stream_handle(x.device))),
-        "xb_fused_forward_d128",
+            _ptr(ws), ws_bytes, stream_handle(x.device))),
+        "xb_fused_forward_d128_ws",
     )
     return out
+
+
+_SPLIT_WORKSPACES: dict = {}
+
+
+def fused_split_workspace(device, batch: int, seq_len: int, num_heads: int, num_layers: int,
+                          causal: bool) -> Optional[torch.Tensor]:
+    """The zero-filled uint8 workspace xb_fused_forward_d128_ws needs for this shape.
+
+    None when the shape runs one workgroup per sequence.  One tensor per
+    (device, size) is kept for the process: every call lowers the hand-off
+    flags it raised, so it is reused as is, but two calls that overlap in time (different
+    streams) must not share it.  Under stream capture no new workspace is
+    made (a capture may not allocate and fill one); the call then runs the
+    one-workgroup form.
+    """
+    need = int(lib().xb_fused_forward_d128_workspace_bytes(
+        int(batch), int(seq_len), int(num_heads), int(num_layers), int(bool(causal))))
+    if need <= 0:
+        return None
+    device = torch.device(device)
+    key = (device.index if device.index is not None else torch.cuda.current_device(), need)
+    ws = _SPLIT_WORKSPACES.get(key)
+    if ws is None:
+        if torch.cuda.is_current_stream_capturing():
+            return None
+        ws = torch.zeros(need, device=device, dtype=torch.uint8)
+        _SPLIT_WORKSPACES[key] = ws
+    return ws
+
+
+def fused_split_timeouts(device=None) -> int:
+    """Hand-offs that timed out, summed over this process's split workspaces on `device`."""
+    total = 0
+    for (index, _), ws in _SPLIT_WORKSPACES.items():
+        if device is None or torch.device(device).index in (None, index):
+            total += int(ws[-4:].view(torch.int32).item())
+    return total

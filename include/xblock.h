@@ -208,6 +208,35 @@ int xb_fused_forward_d128(const float* x, float* y, const void* wpack,
                           int64_t affine_mask, const uint8_t* token_valid,
                           int32_t causal, void* stream);
 
+/*
+ * xb_fused_forward_d128 with a caller workspace that lets small batches use
+ * two workgroups per sequence (tokens 0..63 and 64..127; the first hands each
+ * layer's K and V of its tokens to the second through the workspace), which
+ * doubles the CUs a batch of at most 80 sequences occupies.  Same results,
+ * bit for bit, as xb_fused_forward_d128.
+ *   xb_fused_forward_d128_workspace_bytes: bytes the split needs (0 = this
+ *     shape runs one workgroup per sequence: head_dim above 64, causal = 0,
+ *     seq_len <= 64 or batch > 80).
+ *   workspace: 16-byte aligned, zero-filled before its first use; every call
+ *     lowers the hand-off flags it raised, so the workspace is reused as is
+ *     (hipGraph replays included).  Calls that overlap in time must not
+ *     share one workspace.
+ *     NULL, or a shape that needs none, runs xb_fused_forward_d128; fewer
+ *     than the needed bytes give XB_ERR_WORKSPACE.  Its last 4 bytes count
+ *     hand-offs that timed out (0 when every call was correct).
+ * Replaces the same reference path as xb_fused_forward_d128.
+ */
+int64_t xb_fused_forward_d128_workspace_bytes(int64_t batch, int32_t seq_len,
+                                              int32_t heads, int32_t layers,
+                                              int32_t causal);
+int xb_fused_forward_d128_ws(const float* x, float* y, const void* wpack,
+                             const float* ppack, int64_t batch,
+                             int32_t seq_len, int32_t heads, int32_t ffn_dim,
+                             int32_t layers, int64_t affine_mask,
+                             const uint8_t* token_valid, int32_t causal,
+                             void* workspace, int64_t workspace_bytes,
+                             void* stream);
+
 #ifdef __cplusplus
 }
 #endif

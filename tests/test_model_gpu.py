@@ -438,3 +438,65 @@ def test_fused_stack_masks_and_non_causal(pkg, cuda, geom, causal):
         assert torch.equal(fused[~mask], torch.zeros_like(fused[~mask])), f"{name}: padded rows not zero"
         _check(ref, fused, f"fused {geom} causal={causal} {name}")
         torch.testing.assert_close(fused, per_op, atol=3e-3, rtol=1e-2)
+
+
+@pytest.mark.parametrize(
+    "geom,masked",
+    [((64, 128, 128, 4, 128, 4), False), ((80, 128, 128, 16, 128, 4), False), ((3, 100, 128, 8, 128, 2), True),
+     ((5, 65, 128, 16, 128, 3), False), ((2, 128, 128, 2, 128, 2), True), ((4, 128, 128, 16, 128, 1), False)],
+)
+def test_fused_split_matches_one_workgroup(pkg, cuda, geom, masked):
+    """Two workgroups per sequence (K/V of tokens 0..63 handed over through the
+    workspace) give the one-workgroup kernel's output bit for bit, leave the
+    hand-off flags lowered and count no timed-out hand-off."""
+    kernels = __import__(pkg.__name__ + ".kernels", fromlist=["fused_forward_d128"])
+    config = pkg.TransformerConfig(*geom, True)
+    baseline, optimized = _models(pkg, config, cuda)
+    b, s = geom[0], geom[1]
+    x = torch.randn(b, s, 128, generator=torch.Generator().manual_seed(61))
+    mask = _masks(b, s, 62)["mixed"] if masked else None
+    xg = x.to(cuda)
+    valid = None if mask is None else mask.to(cuda).to(torch.uint8).contiguous()
+    ws = kernels.fused_split_workspace(cuda, b, s, config.num_heads, config.num_layers, True)
+    assert ws is not None and ws.numel() == b * config.num_layers * (2 * 64 * 128 * 2 + 4) + 4
+    wpack, ppack, affine = optimized._fused_stack_parameters()
+    args = dict(num_heads=config.num_heads, ffn_dim=128, num_layers=config.num_layers, affine_mask=affine,
+                token_valid=valid, causal=True)
+    with torch.inference_mode():
+        one = kernels.fused_forward_d128(xg, wpack, ppack, split=False, **args).cpu()
+        for call in range(2):  # the second call reuses the workspace as the first left it
+            two = kernels.fused_forward_d128(xg, wpack, ppack, split=True, **args).cpu()
+            assert torch.equal(one, two), f"{geom} call {call}: split differs, max {(one - two).abs().max()}"
+        flags = ws[b * config.num_layers * 2 * 64 * 128 * 2:]
+        assert int(flags.count_nonzero()) == 0, "hand-off flags not lowered"
+        assert kernels.fused_split_timeouts(cuda) == 0
+        ref = baseline(x, mask)
+    _check(ref, one, f"split {geom} masked={masked}")
+
+
+def test_fused_split_graph_replay_and_smaller_batch(pkg, cuda):
+    """The split form inside a captured graph (workspace made before capture),
+    replayed with eager work between replays, and a smaller batch after it."""
+    kernels = __import__(pkg.__name__ + ".kernels", fromlist=["fused_forward_d128"])
+    config = pkg.TransformerConfig(16, 128, 128, 4, 128, 2, True)
+    _, optimized = _models(pkg, config, cuda)
+    wpack, ppack, affine = optimized._fused_stack_parameters()
+    args = dict(num_heads=4, ffn_dim=128, num_layers=2, affine_mask=affine)
+    xg = torch.randn(16, 128, 128, generator=torch.Generator().manual_seed(71)).to(cuda)
+    with torch.inference_mode():
+        eager = kernels.fused_forward_d128(xg, wpack, ppack, split=False, **args)
+        out = torch.empty_like(xg)
+        kernels.fused_forward_d128(xg, wpack, ppack, out=out, **args)  # makes the workspace outside the capture
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            kernels.fused_forward_d128(xg, wpack, ppack, out=out, **args)
+        for replay in range(3):
+            out.zero_()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager), f"replay {replay}"
+            xg.mul_(1.0)  # eager work between replays
+        small = kernels.fused_forward_d128(xg[:5].contiguous(), wpack, ppack, **args)
+        assert torch.equal(small, eager[:5])
+        assert kernels.fused_split_timeouts(cuda) == 0
