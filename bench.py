@@ -92,11 +92,13 @@ def kernel_costs(name: str, config, rows: int):
         return rows * (10 if name.endswith("_final") else 12) * d, 0.0
     if name.startswith("attention"):
         return rows * 8 * d, 2.0 * b * d * s * (s + 1)
-    if name == "fused_forward_d128":
+    if name in ("fused_forward_d128", "fused_forward_d128_split"):
         layers = config.num_layers
         weights = 2 * layers * (4 * d * d + 2 * d * f)
         attn = 2.0 * b * layers * d * s * (s + 1)
-        return rows * 8 * d + weights, 2.0 * rows * layers * (4 * d * d + 2 * d * f) + attn
+        # split form: per sequence and layer, K and V of tokens 0..63 (FP16) written once and read once
+        handoff = b * layers * 2 * (2 * 64 * d * 2) if name.endswith("_split") else 0
+        return rows * 8 * d + weights + handoff, 2.0 * rows * layers * (4 * d * d + 2 * d * f) + attn
     if name.startswith("gemm_"):
         parts = name.split("_")
         n, k = int(parts[1][1:]), int(parts[2][1:])
@@ -118,7 +120,8 @@ def log(*a):
 
 
 # Kernel symbol substring of each LaunchRecorder name (for counter CSVs).
-KERNEL_SYMBOLS = (("fused_forward_d128", "fused_stack"), ("attention", "attn_kernel"),
+KERNEL_SYMBOLS = (("fused_forward_d128_split", "fused_split"), ("fused_forward_d128", "fused_stack"),
+                  ("attention", "attn_kernel"),
                   ("gemm_", "gemm_"), ("residual_layernorm", "ln_"), ("layernorm", "ln_"))
 CALIBRATION_BYTES = 1 << 30
 
