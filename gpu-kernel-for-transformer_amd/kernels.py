@@ -461,18 +461,20 @@ def fused_split_workspace(device, batch: int, seq_len: int, num_heads: int, num_
     """The zero-filled uint8 workspace xb_fused_forward_d128_ws needs for this shape.
 
     None when the shape runs one workgroup per sequence.  One tensor per
-    (device, size) is kept for the process: every call lowers the hand-off
-    flags it raised, so it is reused as is, but two calls that overlap in time (different
-    streams) must not share it.  Under stream capture no new workspace is
-    made (a capture may not allocate and fill one); the call then runs the
-    one-workgroup form.
+    (device, size, current stream) is kept for the process: every call
+    lowers the hand-off flags it raised, so calls on one stream reuse it as
+    is, and calls on different streams, which may overlap in time, never
+    share one.  Under stream capture no new workspace is made (a capture may
+    not allocate and fill one); the call then runs the one-workgroup form,
+    unless an eager call on the capturing stream made the workspace first.
     """
     need = int(lib().xb_fused_forward_d128_workspace_bytes(
         int(batch), int(seq_len), int(num_heads), int(num_layers), int(bool(causal))))
     if need <= 0:
         return None
     device = torch.device(device)
-    key = (device.index if device.index is not None else torch.cuda.current_device(), need)
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    key = (index, need, stream_handle(torch.device("cuda", index)))
     ws = _SPLIT_WORKSPACES.get(key)
     if ws is None:
         if torch.cuda.is_current_stream_capturing():
@@ -485,7 +487,7 @@ def fused_split_workspace(device, batch: int, seq_len: int, num_heads: int, num_
 def fused_split_timeouts(device=None) -> int:
     """Hand-offs that timed out, summed over this process's split workspaces on `device`."""
     total = 0
-    for (index, _), ws in _SPLIT_WORKSPACES.items():
+    for (index, _, _), ws in _SPLIT_WORKSPACES.items():
         if device is None or torch.device(device).index in (None, index):
             total += int(ws[-4:].view(torch.int32).item())
     return total

@@ -486,10 +486,14 @@ def test_fused_split_graph_replay_and_smaller_batch(pkg, cuda):
     with torch.inference_mode():
         eager = kernels.fused_forward_d128(xg, wpack, ppack, split=False, **args)
         out = torch.empty_like(xg)
-        kernels.fused_forward_d128(xg, wpack, ppack, out=out, **args)  # makes the workspace outside the capture
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):  # makes the capturing stream's workspace outside the capture
+            kernels.fused_forward_d128(xg, wpack, ppack, out=out, **args)
+            assert kernels.fused_split_workspace(cuda, 16, 128, 4, 2, True) is not None
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
+        with torch.cuda.graph(graph, stream=side):
             kernels.fused_forward_d128(xg, wpack, ppack, out=out, **args)
         for replay in range(3):
             out.zero_()
