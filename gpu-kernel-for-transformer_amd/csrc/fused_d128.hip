@@ -707,7 +707,7 @@ __device__ __forceinline__ void attend_pair(const Lds& L, const half8_t (&qop)[N
 // bounded; running out counts an error in `errors` and goes on.
 struct SplitExchange {
   half_t* kv;      // [batch][layers][2][64 * 128]
-  int* flags;      // [batch][layers]
+  int* flags;      // [batch][layers] (room for the largest split batch)
   int* errors;     // one counter
   int layers;
 };
@@ -1094,9 +1094,15 @@ constexpr int64_t kSplitMaxBatch = 80;
 static bool use_split(int64_t batch, int S, int hd, int causal) {
   return hd <= 64 && causal && S > 64 && batch <= kSplitMaxBatch;
 }
+// Workspace layout, the same for every batch of a layer count (so a workspace
+// made for the largest split batch serves all of them): the timeout counter,
+// the flags of kSplitMaxBatch sequences, then from a 256-byte boundary the K/V
+// slots of the batch.
+static int64_t split_kv_offset(int layers) {
+  return ((int64_t)sizeof(int) * (1 + kSplitMaxBatch * layers) + 255) / 256 * 256;
+}
 static int64_t split_workspace_bytes(int64_t batch, int layers) {
-  // K/V slots, then one flag per slot, then the timeout counter (the last 4 bytes).
-  return batch * layers * (2 * 64 * 128 * (int64_t)sizeof(half_t) + (int64_t)sizeof(int)) + (int64_t)sizeof(int);
+  return split_kv_offset(layers) + batch * layers * 2 * 64 * 128 * (int64_t)sizeof(half_t);
 }
 
 template <int HD>
@@ -1106,10 +1112,8 @@ static hipError_t launch(const float* x, float* y, const half_t* w, const float*
   if constexpr (HD <= 64) {
     if (workspace != nullptr) {  // the caller checked use_split and the workspace size
       char* ws = static_cast<char*>(workspace);
-      const int64_t kv_bytes = batch * layers * 2 * 64 * 128 * (int64_t)sizeof(half_t);
-      const w8x2::SplitExchange ex{reinterpret_cast<half_t*>(ws), reinterpret_cast<int*>(ws + kv_bytes),
-                                   reinterpret_cast<int*>(ws + kv_bytes + batch * layers * (int64_t)sizeof(int)),
-                                   layers};
+      const w8x2::SplitExchange ex{reinterpret_cast<half_t*>(ws + split_kv_offset(layers)),
+                                   reinterpret_cast<int*>(ws) + 1, reinterpret_cast<int*>(ws), layers};
       const dim3 grid((unsigned)(2 * batch)), block(64 * w8x2::NW);
       if (token_valid != nullptr)
         hipLaunchKernelGGL((w8x2::fused_split_kernel<HD, 1>), grid, block, 0, s, x, y, w, p, S, layers, affine_mask,

@@ -454,14 +454,17 @@ def fused_forward_d128(
 
 
 _SPLIT_WORKSPACES: dict = {}
+_SPLIT_MAX_BATCH = 80  # the largest batch xb_fused_forward_d128_ws splits
 
 
 def fused_split_workspace(device, batch: int, seq_len: int, num_heads: int, num_layers: int,
                           causal: bool) -> Optional[torch.Tensor]:
     """The zero-filled uint8 workspace xb_fused_forward_d128_ws needs for this shape.
 
-    None when the shape runs one workgroup per sequence.  One tensor per
-    (device, size, current stream) is kept for the process: every call
+    None when the shape runs one workgroup per sequence.  The workspace
+    layout depends only on the layer count, so one tensor per (device,
+    current stream, layers), sized for the largest split batch (a few MB per
+    layer count), serves every batch and is kept for the process: every call
     lowers the hand-off flags it raised, so calls on one stream reuse it as
     is, and calls on different streams, which may overlap in time, never
     share one.  Under stream capture no new workspace is made (a capture may
@@ -474,13 +477,17 @@ def fused_split_workspace(device, batch: int, seq_len: int, num_heads: int, num_
         return None
     device = torch.device(device)
     index = device.index if device.index is not None else torch.cuda.current_device()
-    key = (index, need, stream_handle(torch.device("cuda", index)))
+    key = (index, stream_handle(torch.device("cuda", index)), int(num_layers))
     ws = _SPLIT_WORKSPACES.get(key)
     if ws is None:
         if torch.cuda.is_current_stream_capturing():
             return None
-        ws = torch.zeros(need, device=device, dtype=torch.uint8)
+        size = int(lib().xb_fused_forward_d128_workspace_bytes(
+            _SPLIT_MAX_BATCH, int(seq_len), int(num_heads), int(num_layers), int(bool(causal))))
+        ws = torch.zeros(max(size, need), device=device, dtype=torch.uint8)
         _SPLIT_WORKSPACES[key] = ws
+    if ws.numel() < need:
+        raise RuntimeError(f"split workspace of {ws.numel()} bytes is below the {need} this call needs")
     return ws
 
 
@@ -489,5 +496,5 @@ def fused_split_timeouts(device=None) -> int:
     total = 0
     for (index, _, _), ws in _SPLIT_WORKSPACES.items():
         if device is None or torch.device(device).index in (None, index):
-            total += int(ws[-4:].view(torch.int32).item())
+            total += int(ws[:4].view(torch.int32).item())
     return total

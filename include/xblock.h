@@ -222,8 +222,10 @@ int xb_fused_forward_d128(const float* x, float* y, const void* wpack,
  *     (hipGraph replays included).  Calls that overlap in time must not
  *     share one workspace.
  *     NULL, or a shape that needs none, runs xb_fused_forward_d128; fewer
- *     than the needed bytes give XB_ERR_WORKSPACE.  Its last 4 bytes count
- *     hand-offs that timed out (0 when every call was correct).
+ *     than the needed bytes give XB_ERR_WORKSPACE.  Its layout depends only
+ *     on `layers`, so a workspace sized for a larger batch serves a smaller
+ *     one (the size for batch 80 serves every split batch).  Its first 4
+ *     bytes count hand-offs that timed out (0 when every call was correct).
  * Replaces the same reference path as xb_fused_forward_d128.
  */
 int64_t xb_fused_forward_d128_workspace_bytes(int64_t batch, int32_t seq_len,
