@@ -455,6 +455,7 @@ def fused_forward_d128(
 
 _SPLIT_WORKSPACES: dict = {}
 _SPLIT_MAX_BATCH = 80  # the largest batch xb_fused_forward_d128_ws splits
+_SPLIT_RETIRED: list = []
 
 
 def fused_split_workspace(device, batch: int, seq_len: int, num_heads: int, num_layers: int,
@@ -486,8 +487,12 @@ def fused_split_workspace(device, batch: int, seq_len: int, num_heads: int, num_
             _SPLIT_MAX_BATCH, int(seq_len), int(num_heads), int(num_layers), int(bool(causal))))
         ws = torch.zeros(max(size, need), device=device, dtype=torch.uint8)
         _SPLIT_WORKSPACES[key] = ws
-    if ws.numel() < need:
-        raise RuntimeError(f"split workspace of {ws.numel()} bytes is below the {need} this call needs")
+    if ws.numel() < need:  # only if the library splits larger batches than _SPLIT_MAX_BATCH
+        if torch.cuda.is_current_stream_capturing():
+            return None
+        _SPLIT_RETIRED.append(ws)  # a captured graph may still use it: never freed
+        ws = torch.zeros(need, device=device, dtype=torch.uint8)
+        _SPLIT_WORKSPACES[key] = ws
     return ws
 
 
