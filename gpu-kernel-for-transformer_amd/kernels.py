@@ -454,7 +454,7 @@ def fused_forward_d128(
 
 
 _SPLIT_WORKSPACES: dict = {}
-_SPLIT_MAX_BATCH = 80  # the largest batch xb_fused_forward_d128_ws splits
+_SPLIT_MAX_BATCHES = (128, 96, 80)  # the largest split batch at head_dim 8, 16, and above
 _SPLIT_RETIRED: list = []
 
 
@@ -483,11 +483,11 @@ def fused_split_workspace(device, batch: int, seq_len: int, num_heads: int, num_
     if ws is None:
         if torch.cuda.is_current_stream_capturing():
             return None
-        size = int(lib().xb_fused_forward_d128_workspace_bytes(
-            _SPLIT_MAX_BATCH, int(seq_len), int(num_heads), int(num_layers), int(bool(causal))))
+        size = max(int(lib().xb_fused_forward_d128_workspace_bytes(
+            b, int(seq_len), int(num_heads), int(num_layers), int(bool(causal)))) for b in _SPLIT_MAX_BATCHES)
         ws = torch.zeros(max(size, need), device=device, dtype=torch.uint8)
         _SPLIT_WORKSPACES[key] = ws
-    if ws.numel() < need:  # only if the library splits larger batches than _SPLIT_MAX_BATCH
+    if ws.numel() < need:  # only if the library splits larger batches than _SPLIT_MAX_BATCHES
         if torch.cuda.is_current_stream_capturing():
             return None
         _SPLIT_RETIRED.append(ws)  # a captured graph may still use it: never freed

@@ -212,11 +212,12 @@ int xb_fused_forward_d128(const float* x, float* y, const void* wpack,
  * xb_fused_forward_d128 with a caller workspace that lets small batches use
  * two workgroups per sequence (tokens 0..63 and 64..127; the first hands each
  * layer's K and V of its tokens to the second through the workspace), which
- * doubles the CUs a batch of at most 80 sequences occupies.  Same results,
+ * doubles the CUs a small batch occupies (at most 80 sequences; 96 at
+ * head_dim 16, 128 at head_dim 8).  Same results,
  * bit for bit, as xb_fused_forward_d128.
  *   xb_fused_forward_d128_workspace_bytes: bytes the split needs (0 = this
  *     shape runs one workgroup per sequence: head_dim above 64, causal = 0,
- *     seq_len <= 64 or batch > 80).
+ *     seq_len <= 64 or a batch above those limits).
  *   workspace: 16-byte aligned, zero-filled before its first use; every call
  *     lowers the hand-off flags it raised, so the workspace is reused as is
  *     (hipGraph replays included).  Calls that overlap in time must not
@@ -224,7 +225,7 @@ int xb_fused_forward_d128(const float* x, float* y, const void* wpack,
  *     NULL, or a shape that needs none, runs xb_fused_forward_d128; fewer
  *     than the needed bytes give XB_ERR_WORKSPACE.  Its layout depends only
  *     on `layers`, so a workspace sized for a larger batch serves a smaller
- *     one (the size for batch 80 serves every split batch).  Its first 4
+ *     one (the size for the largest split batch serves every batch).  Its first 4
  *     bytes count hand-offs that timed out (0 when every call was correct).
  * Replaces the same reference path as xb_fused_forward_d128.
  */

@@ -166,12 +166,16 @@ def test_argument_errors_need_no_gpu(capi):
     assert lib.xb_residual_layernorm_masked(16, 16, 1, None, None, None, 16, 1, 4, 128, 1e-5, 0, None, 2, None) == -1
     assert lib.xb_residual_layernorm_masked(16, 16, 1, None, None, None, 16, 1, 0, 128, 1e-5, 0, None, 7, None) == 0
     # Fused d128 stack: which shapes split over two workgroups, and the workspace checks.
-    # Layout: timeout counter, flags of 80 sequences x layers, K/V slots from a 256-byte boundary.
+    # Layout: timeout counter, flags of 128 sequences x layers, K/V slots from a 256-byte boundary.
     slot = 2 * 64 * 128 * 2
-    head = lambda layers: (4 * (1 + 80 * layers) + 255) // 256 * 256
+    head = lambda layers: (4 * (1 + 128 * layers) + 255) // 256 * 256
     assert lib.xb_fused_forward_d128_workspace_bytes(64, 128, 4, 4, 1) == head(4) + 64 * 4 * slot
-    assert lib.xb_fused_forward_d128_workspace_bytes(80, 65, 16, 2, 1) == head(2) + 80 * 2 * slot
-    assert lib.xb_fused_forward_d128_workspace_bytes(81, 128, 4, 4, 1) == 0    # no gain from here on
+    assert lib.xb_fused_forward_d128_workspace_bytes(80, 65, 4, 2, 1) == head(2) + 80 * 2 * slot
+    assert lib.xb_fused_forward_d128_workspace_bytes(81, 128, 4, 4, 1) == 0    # head_dim 32: no gain from here on
+    assert lib.xb_fused_forward_d128_workspace_bytes(96, 128, 8, 4, 1) == head(4) + 96 * 4 * slot   # head_dim 16
+    assert lib.xb_fused_forward_d128_workspace_bytes(97, 128, 8, 4, 1) == 0
+    assert lib.xb_fused_forward_d128_workspace_bytes(128, 128, 16, 4, 1) == head(4) + 128 * 4 * slot  # head_dim 8
+    assert lib.xb_fused_forward_d128_workspace_bytes(129, 128, 16, 4, 1) == 0
     assert lib.xb_fused_forward_d128_workspace_bytes(64, 64, 4, 4, 1) == 0     # no second half
     assert lib.xb_fused_forward_d128_workspace_bytes(64, 128, 4, 4, 0) == 0    # non-causal
     assert lib.xb_fused_forward_d128_workspace_bytes(64, 128, 1, 4, 1) == 0    # head_dim 128
