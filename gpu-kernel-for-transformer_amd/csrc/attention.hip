@@ -448,7 +448,7 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
   constexpr int KT = C::KT, CPK = C::CPK, CH = C::CH;
   static_assert(HD == 64 && C::HDP == 64 && C::HDV == 64, "128-byte rows");
   static_assert(BKEYS == 8 * NW, "one 8-row load per wave per tile");
-  constexpr int NBUF = 3;
+  constexpr int NBUF = 4;
   constexpr int ROW = HD;  // halves per LDS row
 
   __shared__ __attribute__((aligned(1024))) half_t k_lds[NBUF][BKEYS * ROW];
@@ -513,7 +513,7 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
   const int ld_row = 8 * wave + lane / 8, ld_chunk = (lane % 8) ^ (lane / 8);
   auto dma_tile = [&](int t) {  // tile t into buffer t % NBUF
     const int64_t off = (int64_t)min(t * BKEYS + ld_row, S_k - 1) * k_rstride + 8 * ld_chunk;
-    const int buf = t % NBUF;
+    const int buf = t & (NBUF - 1);
     dma16_untracked(kbase + off, &k_lds[buf][8 * wave * ROW]);
     dma16_untracked(vbase + off, &v_lds[buf][8 * wave * ROW]);
   };
@@ -527,6 +527,16 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
   // ... except at the end of odd half-steps, where they must have landed.
   auto tile_barrier = [] {
     __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (0 << 8) | (0 << 14));  // vmcnt(0) expcnt(7) lgkmcnt(0)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  // With the tile after next in flight (its two loads are this wave's newest).
+  auto tile_barrier_ahead = [](bool ahead) {
+    if (ahead)
+      __builtin_amdgcn_s_waitcnt(2 | (7 << 4) | (0 << 8) | (0 << 14));  // vmcnt(2) expcnt(7) lgkmcnt(0)
+    else
+      __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (0 << 8) | (0 << 14));
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
@@ -549,7 +559,7 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
     // Row 16 jb + r16, chunk 4 ks + g, in slot (4 ks + g) ^ (r16 & 7).
     int ql = lane, kc = g ^ (r16 & 7), kr = r16 * ROW;
     asm volatile("" : "+v"(ql), "+v"(kc), "+v"(kr));
-    const half_t* kt_lds = k_lds[t % NBUF];
+    const half_t* kt_lds = k_lds[t & (NBUF - 1)];
     const half_t* kp[KSTEPS] = {kt_lds + kr + 8 * kc, kt_lds + kr + 8 * (kc ^ 4)};
     half8_t qf[NQ][KSTEPS];
 #pragma unroll
@@ -671,28 +681,30 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
   };
 
   if (n_tiles > 0) dma_tile(0);
-  __builtin_amdgcn_s_waitcnt(0);  // tile 0 and the Q operands have landed
-  __syncthreads();
+  if (1 < n_tiles) dma_tile(1);
+  tile_barrier_ahead(1 < n_tiles);  // tile 0 and the Q operands have landed
   // The two groups run separate copies of the loop, each passing the same
   // 2 (n_tiles + 1) barriers, rotated so that only the probabilities (not the
-  // scores) cross the back edge.  Every wave issues its share of tile t+1's
-  // loads at the start of half-step 2t (group B: at the end of its softmax,
-  // once its PV of tile t-2 is done) and waits for them at the end of 2t+1.
+  // scores) cross the back edge.  Every wave issues its share of tile t+2's
+  // loads at the start of half-step 2t (into the buffer of tile t-2, which
+  // every wave left at the end of 2t-1) and waits for tile t+1's at the end
+  // of 2t+1, with tile t+2's still in flight (four buffers: one tile more of
+  // latency hidden than with three, 1% faster on cfg5).
   if (group_a) {
     for (int t = 0; t <= n_tiles; ++t) {
-      if (t + 1 < n_tiles) dma_tile(t + 1);
+      if (t + 2 < n_tiles) dma_tile(t + 2);
       mfma_phase(t);  // half-step 2t: PV(t-1) + QK(t)
       half_step_barrier();
       if (active(t)) softmax(t);  // half-step 2t+1
-      tile_barrier();
+      tile_barrier_ahead(t + 2 < n_tiles);
     }
   } else {
-    if (1 < n_tiles) dma_tile(1);
+    if (2 < n_tiles) dma_tile(2);
     half_step_barrier();  // half-step 0: nothing to exponentiate yet
     for (int t = 0; t < n_tiles; ++t) {
       mfma_phase(t);  // half-step 2t+1: PV(t-1) + QK(t)
-      tile_barrier();
-      if (t + 2 < n_tiles) dma_tile(t + 2);
+      tile_barrier_ahead(t + 2 < n_tiles);
+      if (t + 3 < n_tiles) dma_tile(t + 3);
       if (active(t)) softmax(t);  // half-step 2t+2
       half_step_barrier();
     }
