@@ -25,7 +25,7 @@ LIBRARY_PATH = Path(
 )
 
 # Constants mirrored from include/xblock.h.
-XB_ABI_VERSION = 1
+XB_ABI_VERSION = 2
 XB_F32 = 0
 XB_F16 = 1
 XB_EPI_BIAS = 0
@@ -35,6 +35,8 @@ XB_PACK_NATURAL = 1
 XB_MASK_UPDATE = 1
 XB_MASK_SUM = 2
 XB_MASK_OUTPUT = 4
+XB_SPLIT_SPINS_DEFAULT = -1
+XB_SPLIT_FAULT_NO_PUBLISH = 1
 
 EXPORTED_SYMBOLS = (
     "xb_abi_version",
@@ -85,7 +87,7 @@ _SIGNATURES = {
     "xb_fused_forward_d128_workspace_bytes": (_i64, [_i64, _i32, _i32, _i32, _i32]),
     "xb_fused_forward_d128_ws": (
         ctypes.c_int,
-        [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i64, _vp, _i32, _vp, _i64, _vp],
+        [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i64, _vp, _i32, _vp, _i64, _i32, _i32, _vp],
     ),
 }
 

@@ -982,10 +982,13 @@ extern "C" int64_t xb_attention_kv_cache_workspace_bytes(int32_t batch, int64_t 
   return decode_geometry(batch, heads, (int)(start + chunk), head_dim).bytes;
 }
 
-extern "C" int xb_attention_kv_cache(const void* qkv, const void* k_cache, const void* v_cache, void* out,
-                                     int32_t batch, int64_t chunk, int32_t heads, int32_t head_dim, int64_t start,
-                                     int64_t capacity, float scale, void* workspace, int64_t workspace_bytes,
-                                     void* stream) {
+// The cached-attention call behind xb_attention_kv_cache and its no-allocation
+// variant.  `workspace_of(bytes, &ptr)` supplies the decode partials' memory
+// (or an error code) once the call has been validated and sized.
+template <typename WorkspaceOf>
+static int attention_kv_cache(const void* qkv, const void* k_cache, const void* v_cache, void* out, int32_t batch,
+                              int64_t chunk, int32_t heads, int32_t head_dim, int64_t start, int64_t capacity,
+                              float scale, void* stream, WorkspaceOf&& workspace_of) {
   const int bad = check_cache_args(batch, chunk, heads, head_dim, start, capacity);
   if (bad) return bad;
   if (batch == 0 || chunk == 0) return XB_OK;
@@ -1013,8 +1016,22 @@ extern "C" int xb_attention_kv_cache(const void* qkv, const void* k_cache, const
   if (chunk > kDecodeQueries)
     return (int)by_head_dim(head_dim, [&](auto hd) { return dispatch_attn<decltype(hd)::value>(a, batch, 1, s); });
   const DecodeGeometry geo = decode_geometry(batch, heads, a.S_k, head_dim);
-  if (!workspace) return XB_ERR_NULL_POINTER;
-  if (workspace_bytes < geo.bytes) return XB_ERR_WORKSPACE;
-  if ((uintptr_t)workspace & 15u) return XB_ERR_MISALIGNED;
+  void* workspace = nullptr;
+  const int got = workspace_of(geo.bytes, &workspace);
+  if (got != XB_OK) return got;
   return (int)by_head_dim(head_dim, [&](auto hd) { return launch_decode<decltype(hd)::value>(a, batch, geo, workspace, s); });
+}
+
+extern "C" int xb_attention_kv_cache(const void* qkv, const void* k_cache, const void* v_cache, void* out,
+                                     int32_t batch, int64_t chunk, int32_t heads, int32_t head_dim, int64_t start,
+                                     int64_t capacity, float scale, void* workspace, int64_t workspace_bytes,
+                                     void* stream) {
+  return attention_kv_cache(qkv, k_cache, v_cache, out, batch, chunk, heads, head_dim, start, capacity, scale, stream,
+                            [&](int64_t need, void** ptr) {
+                              if (!workspace) return XB_ERR_NULL_POINTER;
+                              if (workspace_bytes < need) return XB_ERR_WORKSPACE;
+                              if ((uintptr_t)workspace & 15u) return XB_ERR_MISALIGNED;
+                              *ptr = workspace;
+                              return XB_OK;
+                            });
 }

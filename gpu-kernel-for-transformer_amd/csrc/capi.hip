@@ -15,7 +15,7 @@ extern "C" const char* xb_strerror(int code) {
     case XB_ERR_BAD_DTYPE: return "xblock: unsupported element type";
     case XB_ERR_UNSUPPORTED_SHAPE: return "xblock: unsupported shape (see include/xblock.h)";
     case XB_ERR_MISALIGNED: return "xblock: a pointer is not 16-byte aligned";
-    case XB_ERR_BAD_EPILOGUE: return "xblock: unknown GEMM epilogue or mask mode";
+    case XB_ERR_BAD_EPILOGUE: return "xblock: unknown GEMM epilogue, mask mode or flag";
     case XB_ERR_WORKSPACE: return "xblock: workspace smaller than the call needs";
     default:
       if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));

@@ -436,6 +436,7 @@ struct Lds {
   float prm[2][P_LAYER];                               // per-layer vectors, by layer parity
   float2 xstat[2][XSTAT];                              // LayerNorm partial statistics (LN1 / LN2)
   uint8_t kval[SMAX];                                  // MASKED: token t may be attended to / is output
+  int poison;                                          // split form: a K/V hand-off of this block timed out
 };
 
 // Causal attention of query block QB (keys 0 .. 16 QB + 15) for the heads of
@@ -699,21 +700,53 @@ __device__ __forceinline__ void attend_pair(const Lds& L, const half8_t (&qop)[N
 
 // K/V exchange of the split form.  Per (sequence, layer) a 32 KB slot: K rows
 // of tokens 0..63 ([64][128] halves) then their V^T columns ([128][64]), and
-// an int flag; part 0 stores the slot and raises the flag (release, agent
-// scope), part 1 waits for it (acquire), copies the slot into its LDS and
-// lowers the flag again, so every flag is back to zero when the kernel ends
-// (graph replays reuse the workspace as it is).  Part 1 only waits on part 0, which has the
-// lower block index and so was dispatched first: the wait ends.  It is still
-// bounded; running out counts an error in `errors` and goes on.
-struct SplitExchange {
-  half_t* kv;      // [batch][layers][2][64 * 128]
-  int* flags;      // [batch][layers] (room for the largest split batch)
-  int* errors;     // one counter
-  int layers;
+// a 64-bit flag.  Every launch has its own epoch, the workspace's generation
+// plus one: part 0 stores the slot and then the epoch into the flag (release,
+// agent scope); part 1 waits until the flag holds this launch's epoch
+// (acquire) and copies the slot into its LDS.  A flag left by an earlier
+// launch holds an older epoch and never satisfies a later wait, so nothing
+// has to be lowered again and a late producer cannot feed the next call.  The
+// last block of the grid to finish (a counter of finished blocks) advances the
+// generation; the next launch on the stream starts after this one has ended,
+// so every block of a launch reads the same generation.
+//
+// Forward progress: part 1 of sequence b only waits on part 0 of b.  The host
+// places them on one XCD (blocks b and R + b with R a multiple of the eight
+// XCDs, which receive blocks round-robin) where part 0 has the lower index, so
+// that XCD's in-order dispatcher started part 0 first; part 0 never waits.
+// The wait is still bounded (spin_limit sleeps): a wait that runs out counts
+// an error in the header, poisons the block (its output rows become NaN) and
+// goes on, so every wave of the grid ends.
+struct SplitHeader {
+  int errors;                      // hand-offs that timed out, over all launches
+  unsigned done;                   // blocks of the current launch that finished
+  unsigned long long generation;   // launches completed on this workspace
 };
-constexpr int kExchangeSpins = 1 << 20;
+struct SplitExchange {
+  half_t* kv;                      // [batch][layers][2][64 * 128]
+  unsigned long long* flags;       // [kSplitMaxBatch][layers]: epoch of the last publish
+  SplitHeader* hdr;
+  int layers;
+  int spin_limit;                  // sleeps before a wait gives up
+  int skip_publish;                // fault injection: part 0 never raises its flags
+};
 
-__device__ __forceinline__ void publish_kv(const Lds& L, const SplitExchange& ex, int64_t seq, int layer) {
+__device__ __forceinline__ unsigned long long split_epoch(const SplitExchange& ex) {
+  return __hip_atomic_load(&ex.hdr->generation, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
+}
+
+// Thread 0 of every block, last thing: the grid's last block resets the
+// counter and publishes the generation the next launch starts from.
+__device__ __forceinline__ void split_block_done(const SplitExchange& ex, unsigned long long epoch) {
+  const unsigned prev = __hip_atomic_fetch_add(&ex.hdr->done, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+  if (prev == gridDim.x - 1) {
+    __hip_atomic_store(&ex.hdr->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&ex.hdr->generation, epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+__device__ __forceinline__ void publish_kv(const Lds& L, const SplitExchange& ex, int64_t seq, int layer,
+                                           unsigned long long epoch) {
   half_t* slot = ex.kv + (seq * ex.layers + layer) * (2 * 64 * 128);
   const int t = threadIdx.x;  // 512 threads, two 16-byte chunks of K and two of V^T each
 #pragma unroll
@@ -724,21 +757,25 @@ __device__ __forceinline__ void publish_kv(const Lds& L, const SplitExchange& ex
         *reinterpret_cast<const half8_t*>(L.vt + (e / 8) * LD + 8 * (e % 8));
   }
   __syncthreads();  // every thread's stores are done
-  if (t == 0) __hip_atomic_store(ex.flags + seq * ex.layers + layer, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  if (t == 0 && !ex.skip_publish)
+    __hip_atomic_store(ex.flags + seq * ex.layers + layer, epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ void fetch_kv(Lds& L, const SplitExchange& ex, int64_t seq, int layer) {
+__device__ __forceinline__ void fetch_kv(Lds& L, const SplitExchange& ex, int64_t seq, int layer,
+                                         unsigned long long epoch) {
   const half_t* slot = ex.kv + (seq * ex.layers + layer) * (2 * 64 * 128);
-  int* flag = ex.flags + seq * ex.layers + layer;
+  unsigned long long* flag = ex.flags + seq * ex.layers + layer;
   const int t = threadIdx.x;
   if (t == 0) {
     int spins = 0;
-    while (__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) == 0) {
-      __builtin_amdgcn_s_sleep(1);
-      if (++spins > kExchangeSpins) {
-        atomicAdd(ex.errors, 1);
+    while (__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) != epoch) {
+      if (spins >= ex.spin_limit) {
+        atomicAdd(&ex.hdr->errors, 1);
+        L.poison = 1;
         break;
       }
+      __builtin_amdgcn_s_sleep(1);
+      ++spins;
     }
   }
   __syncthreads();
@@ -749,8 +786,7 @@ __device__ __forceinline__ void fetch_kv(Lds& L, const SplitExchange& ex, int64_
     *reinterpret_cast<half8_t*>(L.vt + (e / 8) * LD + 8 * (e % 8)) =
         *reinterpret_cast<const half8_t*>(slot + 64 * 128 + 8 * e);
   }
-  __syncthreads();  // the fetched rows are in LDS (and the slot is read)
-  if (t == 0) __hip_atomic_store(flag, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();  // the fetched rows are in LDS
 }
 
 // NBT = 2: the pair form above (blocks pair, 7 - pair per wave, one workgroup
@@ -762,7 +798,8 @@ template <int HD, int HALF, int MASK, int NBT, bool SPLIT>
 __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ x, float* __restrict__ y,
                                               const half_t* __restrict__ wpack, const float* __restrict__ ppack,
                                               int S, int layers, int64_t affine_mask, int wave, int pair,
-                                              int64_t seq, int part, const SplitExchange& ex) {
+                                              int64_t seq, int part, const SplitExchange& ex,
+                                              unsigned long long epoch) {
   constexpr int H = D / HD;
   static_assert(H >= 2, "heads split between the two halves");
   constexpr int half = HALF;
@@ -888,9 +925,9 @@ __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ 
     lds_barrier();  // K and V^T of every token block are in LDS
     if constexpr (SPLIT) {
       if (part == 0)
-        publish_kv(L, ex, seq, layer);
+        publish_kv(L, ex, seq, layer, epoch);
       else
-        fetch_kv(L, ex, seq, layer);
+        fetch_kv(L, ex, seq, layer, epoch);
     }
 
     // ---- causal attention of both blocks, own heads --------------------------
@@ -995,6 +1032,8 @@ __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ 
   int lane_o = lane;
   asm volatile("" : "+v"(lane_o));
   const int g_o = lane_o / 16;
+  // A timed-out hand-off left this block with K/V of unknown content: its rows leave as NaN.
+  const bool poisoned = SPLIT && L.poison != 0;
 #pragma unroll
   for (int b = 0; b < NBT; ++b) {
     const int tok_o = 16 * tb[b] + lane_o % 16;
@@ -1009,7 +1048,10 @@ __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ 
         float4_t o;
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[i] = zero ? 0.f : (res[b][j][i] - mean[b]) * rstd[b] * gg[i] + bb[i];
-        *reinterpret_cast<float4_t*>(yrow + f0) = o;
+        if (poisoned)  // quiet NaN bit patterns, stored as integers (this file compiles without NaN semantics)
+          *reinterpret_cast<uint4*>(yrow + f0) = make_uint4(0x7fc00000u, 0x7fc00000u, 0x7fc00000u, 0x7fc00000u);
+        else
+          *reinterpret_cast<float4_t*>(yrow + f0) = o;
       }
     }
   }
@@ -1029,25 +1071,34 @@ __global__ __launch_bounds__(64 * NW, 1) void fused_stack8x2_kernel(
   }
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int pair = wave % 4;  // waves w and w + 4 (the two halves of blocks pair, 7 - pair) share a SIMD
-  const SplitExchange none{nullptr, nullptr, nullptr, 0};
+  const SplitExchange none{nullptr, nullptr, nullptr, 0, 0, 0};
   if (wave < 4)
-    stack8x2_body<HD, 0, MASK, 2, false>(lds, x, y, wpack, ppack, S, layers, affine_mask, wave, pair, blockIdx.x, 0, none);
+    stack8x2_body<HD, 0, MASK, 2, false>(lds, x, y, wpack, ppack, S, layers, affine_mask, wave, pair, blockIdx.x, 0, none, 0);
   else
-    stack8x2_body<HD, 1, MASK, 2, false>(lds, x, y, wpack, ppack, S, layers, affine_mask, wave, pair, blockIdx.x, 0, none);
+    stack8x2_body<HD, 1, MASK, 2, false>(lds, x, y, wpack, ppack, S, layers, affine_mask, wave, pair, blockIdx.x, 0, none, 0);
 }
 
 // Split form (causal only, MASK 0 or 1): block b < batch is part 0 of
-// sequence b, block batch + b part 1 of it (when batch % 8 == 0 the two share
-// an XCD: blocks are dealt to the eight XCDs round-robin).
+// sequence b, block R + b part 1 of it, R = batch rounded up to the eight
+// XCDs, so both parts of a sequence run on one XCD (blocks are dealt to the
+// XCDs round-robin); blocks b in [batch, R) of either part only count
+// themselves finished.
 template <int HD, int MASK>
 __global__ __launch_bounds__(64 * NW, 1) void fused_split_kernel(
     const float* __restrict__ x, float* __restrict__ y, const half_t* __restrict__ wpack,
     const float* __restrict__ ppack, int S, int layers, int64_t affine_mask,
-    const uint8_t* __restrict__ token_valid, int batch, SplitExchange ex) {
+    const uint8_t* __restrict__ token_valid, int batch, int rounded, SplitExchange ex) {
   static_assert(MASK != 2, "part 0 would need part 1's keys");
   __shared__ Lds lds;
-  const int part = blockIdx.x >= (unsigned)batch ? 1 : 0;
-  const int64_t seq = blockIdx.x - part * batch;
+  const int part = blockIdx.x >= (unsigned)rounded ? 1 : 0;
+  const int64_t seq = blockIdx.x - part * rounded;
+  // Only thread 0 takes part in the hand-off protocol (flags, counters).
+  const unsigned long long epoch = threadIdx.x == 0 ? split_epoch(ex) : 0;
+  if (seq >= batch) {
+    if (threadIdx.x == 0) split_block_done(ex, epoch);
+    return;
+  }
+  if (threadIdx.x == 0) lds.poison = 0;  // visible after the body's first barrier
   if constexpr (MASK != 0) {
     for (int t = threadIdx.x; t < SMAX; t += 64 * NW)
       lds.kval[t] = t < S && (token_valid == nullptr || token_valid[seq * S + t] != 0) ? 1 : 0;
@@ -1055,9 +1106,12 @@ __global__ __launch_bounds__(64 * NW, 1) void fused_split_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int pair = wave % 4;  // block 4 part + pair; waves w and w + 4 (its two halves) share a SIMD
   if (wave < 4)
-    stack8x2_body<HD, 0, MASK, 1, true>(lds, x, y, wpack, ppack, S, layers, affine_mask, wave, pair, seq, part, ex);
+    stack8x2_body<HD, 0, MASK, 1, true>(lds, x, y, wpack, ppack, S, layers, affine_mask, wave, pair, seq, part, ex,
+                                         epoch);
   else
-    stack8x2_body<HD, 1, MASK, 1, true>(lds, x, y, wpack, ppack, S, layers, affine_mask, wave, pair, seq, part, ex);
+    stack8x2_body<HD, 1, MASK, 1, true>(lds, x, y, wpack, ppack, S, layers, affine_mask, wave, pair, seq, part, ex,
+                                         epoch);
+  if (threadIdx.x == 0) split_block_done(ex, epoch);
 }
 
 }  // namespace w8x2
@@ -1098,32 +1152,39 @@ static bool use_split(int64_t batch, int S, int hd, int causal) {
   return hd <= 64 && causal && S > 64 && batch <= split_limit(hd);
 }
 // Workspace layout, the same for every batch of a layer count (so a workspace
-// made for the largest split batch serves all of them): the timeout counter,
-// the flags of kSplitMaxBatch sequences, then from a 256-byte boundary the K/V
-// slots of the batch.
+// made for the largest split batch serves all of them): a 256-byte header
+// (w8x2::SplitHeader: timeout counter, finished blocks, generation), the
+// 64-bit flags of kSplitMaxBatch sequences, then from a 256-byte boundary the
+// K/V slots of the batch.
+constexpr int64_t kSplitHeaderBytes = 256;
 static int64_t split_kv_offset(int layers) {
-  return ((int64_t)sizeof(int) * (1 + kSplitMaxBatch * layers) + 255) / 256 * 256;
+  return (kSplitHeaderBytes + (int64_t)sizeof(unsigned long long) * kSplitMaxBatch * layers + 255) / 256 * 256;
 }
 static int64_t split_workspace_bytes(int64_t batch, int layers) {
   return split_kv_offset(layers) + batch * layers * 2 * 64 * 128 * (int64_t)sizeof(half_t);
 }
+constexpr int kSplitDefaultSpins = 1 << 20;  // about 30-40 ms of s_sleep 1
 
 template <int HD>
 static hipError_t launch(const float* x, float* y, const half_t* w, const float* p, int64_t batch, int S,
                          int layers, int64_t affine_mask, const uint8_t* token_valid, int causal, void* workspace,
-                         hipStream_t s) {
+                         int spin_limit, int fault_flags, hipStream_t s) {
   if constexpr (HD <= 64) {
     if (workspace != nullptr) {  // the caller checked use_split and the workspace size
       char* ws = static_cast<char*>(workspace);
       const w8x2::SplitExchange ex{reinterpret_cast<half_t*>(ws + split_kv_offset(layers)),
-                                   reinterpret_cast<int*>(ws) + 1, reinterpret_cast<int*>(ws), layers};
-      const dim3 grid((unsigned)(2 * batch)), block(64 * w8x2::NW);
+                                   reinterpret_cast<unsigned long long*>(ws + kSplitHeaderBytes),
+                                   reinterpret_cast<w8x2::SplitHeader*>(ws), layers,
+                                   spin_limit < 0 ? kSplitDefaultSpins : spin_limit,
+                                   (fault_flags & XB_SPLIT_FAULT_NO_PUBLISH) ? 1 : 0};
+      const int rounded = (int)((batch + 7) / 8 * 8);  // both parts of a sequence on one XCD
+      const dim3 grid((unsigned)(2 * rounded)), block(64 * w8x2::NW);
       if (token_valid != nullptr)
         hipLaunchKernelGGL((w8x2::fused_split_kernel<HD, 1>), grid, block, 0, s, x, y, w, p, S, layers, affine_mask,
-                           token_valid, (int)batch, ex);
+                           token_valid, (int)batch, rounded, ex);
       else
         hipLaunchKernelGGL((w8x2::fused_split_kernel<HD, 0>), grid, block, 0, s, x, y, w, p, S, layers, affine_mask,
-                           token_valid, (int)batch, ex);
+                           token_valid, (int)batch, rounded, ex);
       return hipGetLastError();
     }
     const dim3 grid((unsigned)batch), block(64 * w8x2::NW);
@@ -1164,7 +1225,7 @@ extern "C" int xb_pack_linear_fragments(const float* w, void* out, int32_t n, in
 static int fused_forward(const float* x, float* y, const void* wpack, const float* ppack, int64_t batch,
                          int32_t seq_len, int32_t heads, int32_t ffn_dim, int32_t layers, int64_t affine_mask,
                          const uint8_t* token_valid, int32_t causal, void* workspace, int64_t workspace_bytes,
-                         void* stream) {
+                         int32_t spin_limit, int32_t fault_flags, void* stream) {
   if (batch < 0 || seq_len <= 0 || heads <= 0 || ffn_dim <= 0 || layers <= 0) return XB_ERR_BAD_SIZE;
   if (batch > 0x7fffffffLL) return XB_ERR_BAD_SIZE;
   if (seq_len > fused::SMAX || fused::D % heads != 0) return XB_ERR_UNSUPPORTED_SHAPE;
@@ -1172,6 +1233,7 @@ static int fused_forward(const float* x, float* y, const void* wpack, const floa
   if (hd != 8 && hd != 16 && hd != 32 && hd != 64 && hd != 128) return XB_ERR_UNSUPPORTED_SHAPE;
   if (hd == 128 && (token_valid != nullptr || !causal)) return XB_ERR_UNSUPPORTED_SHAPE;  // eight-wave kernel: causal only
   if (ffn_dim != 128) return XB_ERR_UNSUPPORTED_SHAPE;
+  if (fault_flags & ~XB_SPLIT_FAULT_NO_PUBLISH) return XB_ERR_BAD_EPILOGUE;
   if (layers > 31) affine_mask = -1;  // bits beyond the mask: always affine
   if (batch == 0) return XB_OK;
   if (!x || !y || !wpack || !ppack) return XB_ERR_NULL_POINTER;
@@ -1186,11 +1248,11 @@ static int fused_forward(const float* x, float* y, const void* wpack, const floa
   const half_t* w = static_cast<const half_t*>(wpack);
   hipError_t e;
   switch (hd) {
-    case 8: e = fused::launch<8>(x, y, w, ppack, batch, seq_len, layers, affine_mask, token_valid, causal, split_ws, s); break;
-    case 16: e = fused::launch<16>(x, y, w, ppack, batch, seq_len, layers, affine_mask, token_valid, causal, split_ws, s); break;
-    case 32: e = fused::launch<32>(x, y, w, ppack, batch, seq_len, layers, affine_mask, token_valid, causal, split_ws, s); break;
-    case 64: e = fused::launch<64>(x, y, w, ppack, batch, seq_len, layers, affine_mask, token_valid, causal, split_ws, s); break;
-    default: e = fused::launch<128>(x, y, w, ppack, batch, seq_len, layers, affine_mask, token_valid, causal, nullptr, s); break;
+    case 8: e = fused::launch<8>(x, y, w, ppack, batch, seq_len, layers, affine_mask, token_valid, causal, split_ws, spin_limit, fault_flags, s); break;
+    case 16: e = fused::launch<16>(x, y, w, ppack, batch, seq_len, layers, affine_mask, token_valid, causal, split_ws, spin_limit, fault_flags, s); break;
+    case 32: e = fused::launch<32>(x, y, w, ppack, batch, seq_len, layers, affine_mask, token_valid, causal, split_ws, spin_limit, fault_flags, s); break;
+    case 64: e = fused::launch<64>(x, y, w, ppack, batch, seq_len, layers, affine_mask, token_valid, causal, split_ws, spin_limit, fault_flags, s); break;
+    default: e = fused::launch<128>(x, y, w, ppack, batch, seq_len, layers, affine_mask, token_valid, causal, nullptr, -1, 0, s); break;
   }
   return (int)e;
 }
@@ -1200,7 +1262,7 @@ extern "C" int xb_fused_forward_d128(const float* x, float* y, const void* wpack
                                      int32_t layers, int64_t affine_mask, const uint8_t* token_valid,
                                      int32_t causal, void* stream) {
   return fused_forward(x, y, wpack, ppack, batch, seq_len, heads, ffn_dim, layers, affine_mask, token_valid, causal,
-                       nullptr, 0, stream);
+                       nullptr, 0, -1, 0, stream);
 }
 
 extern "C" int64_t xb_fused_forward_d128_workspace_bytes(int64_t batch, int32_t seq_len, int32_t heads,
@@ -1212,7 +1274,8 @@ extern "C" int64_t xb_fused_forward_d128_workspace_bytes(int64_t batch, int32_t 
 extern "C" int xb_fused_forward_d128_ws(const float* x, float* y, const void* wpack, const float* ppack,
                                         int64_t batch, int32_t seq_len, int32_t heads, int32_t ffn_dim,
                                         int32_t layers, int64_t affine_mask, const uint8_t* token_valid,
-                                        int32_t causal, void* workspace, int64_t workspace_bytes, void* stream) {
+                                        int32_t causal, void* workspace, int64_t workspace_bytes,
+                                        int32_t spin_limit, int32_t fault_flags, void* stream) {
   return fused_forward(x, y, wpack, ppack, batch, seq_len, heads, ffn_dim, layers, affine_mask, token_valid, causal,
-                       workspace, workspace_bytes, stream);
+                       workspace, workspace_bytes, spin_limit, fault_flags, stream);
 }

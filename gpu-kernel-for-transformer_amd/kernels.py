@@ -421,6 +421,9 @@ def fused_forward_d128(
     token_valid: Optional[torch.Tensor] = None,
     causal: bool = True,
     split: bool = True,
+    strict: bool = False,
+    spin_limit: int = _capi.XB_SPLIT_SPINS_DEFAULT,
+    fault_flags: int = 0,
 ) -> torch.Tensor:
     """Whole-stack forward for d_model 128 / seq_len <= 128 (see xb_fused_forward_d128).
 
@@ -430,8 +433,12 @@ def fused_forward_d128(
     token_valid ([B, S] bool/uint8) and causal=False give the padding and
     non-causal semantics of `attention` (padded rows come out zero).
     split=True lets a small causal batch run two workgroups per sequence
-    (xb_fused_forward_d128_ws) with a zero-filled workspace cached per device
-    and size; the results are the same bit for bit.
+    (xb_fused_forward_d128_ws) with a workspace from `fused_split_workspace`;
+    the results are the same bit for bit.  A hand-off that timed out turns
+    the rows of the waiting workgroup into NaN and counts in the workspace;
+    strict=True also synchronises after the call and raises RuntimeError if
+    the count grew.  spin_limit / fault_flags are passed through (tests force
+    the time-out path with spin_limit=0, fault_flags=XB_SPLIT_FAULT_NO_PUBLISH).
     """
     _require_device(x, "fused_forward_d128")
     if x.ndim != 3 or x.shape[-1] != 128 or x.dtype != torch.float32 or not x.is_contiguous():
@@ -442,35 +449,76 @@ def fused_forward_d128(
     valid = None if token_valid is None else _byte_mask(token_valid, batch * seq_len, x.device, "token_valid")
     ws = fused_split_workspace(x.device, batch, seq_len, num_heads, num_layers, causal) if split else None
     ws_bytes = 0 if ws is None else ws.numel()
+    before = _split_timeouts_of(ws) if (strict and ws is not None) else 0
     check(
         _launch("fused_forward_d128_split" if ws is not None else "fused_forward_d128",
                 lambda: lib().xb_fused_forward_d128_ws(
             x.data_ptr(), out.data_ptr(), wpack.data_ptr(), ppack.data_ptr(), batch, seq_len,
             num_heads, ffn_dim, num_layers, int(affine_mask), _ptr(valid), int(bool(causal)),
-            _ptr(ws), ws_bytes, stream_handle(x.device))),
+            _ptr(ws), ws_bytes, int(spin_limit), int(fault_flags), stream_handle(x.device))),
         "xb_fused_forward_d128_ws",
     )
+    if strict and ws is not None:
+        grown = _split_timeouts_of(ws) - before
+        if grown:
+            raise RuntimeError(f"fused_forward_d128: {grown} split-form K/V hand-off(s) timed out; "
+                               "the affected rows are NaN")
     return out
 
 
-_SPLIT_WORKSPACES: dict = {}
 _SPLIT_MAX_BATCHES = (128, 96, 80)  # the largest split batch at head_dim 8, 16, and above
+_SPLIT_WORKSPACES: dict = {}        # eager calls: (device, stream, layers) -> workspace
 _SPLIT_RETIRED: list = []
+_PRIVATE_POOLS: list = []           # stack of active SplitWorkspacePool scopes
+
+
+class SplitWorkspacePool:
+    """Split-form workspaces owned by one captured graph.
+
+    A hipGraph replays on whatever stream is current at replay time, so a
+    graph must not share a workspace with eager calls (or other graphs) that
+    may run beside it.  While a pool is active (``with pool:``), every split
+    call on the pool's device takes the pool's own workspace for its layer
+    count, made on first use outside capture (the warm-up calls that precede
+    a capture make it); the graph keeps the pool alive.  Replays of one graph
+    must not overlap each other, as for any graph with static buffers.
+    """
+
+    def __init__(self) -> None:
+        self.workspaces: Dict[Tuple[int, int], torch.Tensor] = {}
+
+    def __enter__(self) -> "SplitWorkspacePool":
+        _PRIVATE_POOLS.append(self)
+        return self
+
+    def __exit__(self, *exc) -> None:
+        _PRIVATE_POOLS.remove(self)
+
+    def timeouts(self) -> int:
+        return sum(_split_timeouts_of(ws) for ws in self.workspaces.values())
+
+
+def _new_split_workspace(device: torch.device, seq_len: int, num_heads: int, num_layers: int, causal: bool,
+                         need: int) -> torch.Tensor:
+    size = max(int(lib().xb_fused_forward_d128_workspace_bytes(
+        b, int(seq_len), int(num_heads), int(num_layers), int(bool(causal)))) for b in _SPLIT_MAX_BATCHES)
+    return torch.zeros(max(size, need), device=device, dtype=torch.uint8)
 
 
 def fused_split_workspace(device, batch: int, seq_len: int, num_heads: int, num_layers: int,
                           causal: bool) -> Optional[torch.Tensor]:
     """The zero-filled uint8 workspace xb_fused_forward_d128_ws needs for this shape.
 
-    None when the shape runs one workgroup per sequence.  The workspace
-    layout depends only on the layer count, so one tensor per (device,
-    current stream, layers), sized for the largest split batch (a few MB per
-    layer count), serves every batch and is kept for the process: every call
-    lowers the hand-off flags it raised, so calls on one stream reuse it as
-    is, and calls on different streams, which may overlap in time, never
-    share one.  Under stream capture no new workspace is made (a capture may
-    not allocate and fill one); the call then runs the one-workgroup form,
-    unless an eager call on the capturing stream made the workspace first.
+    None when the shape runs one workgroup per sequence.  The layout depends
+    only on the layer count, so one tensor per (device, current stream,
+    layers), sized for the largest split batch (a few MB), serves every batch
+    and is kept for the process: each launch signals with its own epoch, so
+    calls on one stream reuse it as it is, and calls on different streams,
+    which may overlap in time, never share one.  Inside a
+    `SplitWorkspacePool` scope the pool's workspace is used instead.  Under
+    stream capture outside such a scope no workspace is used (its replays
+    could overlap eager calls that share it): the call then runs the
+    one-workgroup form, with the same results.
     """
     need = int(lib().xb_fused_forward_d128_workspace_bytes(
         int(batch), int(seq_len), int(num_heads), int(num_layers), int(bool(causal))))
@@ -478,28 +526,44 @@ def fused_split_workspace(device, batch: int, seq_len: int, num_heads: int, num_
         return None
     device = torch.device(device)
     index = device.index if device.index is not None else torch.cuda.current_device()
+    capturing = torch.cuda.is_current_stream_capturing()
+    if _PRIVATE_POOLS:
+        pool = _PRIVATE_POOLS[-1]
+        key = (index, int(num_layers))
+        ws = pool.workspaces.get(key)
+        if ws is None or ws.numel() < need:
+            if capturing:
+                return None
+            ws = _new_split_workspace(torch.device("cuda", index), seq_len, num_heads, num_layers, causal, need)
+            pool.workspaces[key] = ws
+        return ws
+    if capturing:
+        return None
     key = (index, stream_handle(torch.device("cuda", index)), int(num_layers))
     ws = _SPLIT_WORKSPACES.get(key)
     if ws is None:
-        if torch.cuda.is_current_stream_capturing():
-            return None
-        size = max(int(lib().xb_fused_forward_d128_workspace_bytes(
-            b, int(seq_len), int(num_heads), int(num_layers), int(bool(causal)))) for b in _SPLIT_MAX_BATCHES)
-        ws = torch.zeros(max(size, need), device=device, dtype=torch.uint8)
+        ws = _new_split_workspace(torch.device("cuda", index), seq_len, num_heads, num_layers, causal, need)
         _SPLIT_WORKSPACES[key] = ws
     if ws.numel() < need:  # only if the library splits larger batches than _SPLIT_MAX_BATCHES
-        if torch.cuda.is_current_stream_capturing():
-            return None
-        _SPLIT_RETIRED.append(ws)  # a captured graph may still use it: never freed
+        _SPLIT_RETIRED.append(ws)  # a graph captured before may still use it: never freed
         ws = torch.zeros(need, device=device, dtype=torch.uint8)
         _SPLIT_WORKSPACES[key] = ws
     return ws
 
 
+def _split_timeouts_of(ws: torch.Tensor) -> int:
+    return int(ws[:4].view(torch.int32).item())
+
+
+def split_launches_of(ws: torch.Tensor) -> int:
+    """Completed split launches on a workspace (its launch generation, bytes 8..15)."""
+    return int(ws[8:16].view(torch.int64).item())
+
+
 def fused_split_timeouts(device=None) -> int:
-    """Hand-offs that timed out, summed over this process's split workspaces on `device`."""
+    """Hand-offs that timed out, summed over this process's eager split workspaces on `device`."""
     total = 0
     for (index, _, _), ws in _SPLIT_WORKSPACES.items():
         if device is None or torch.device(device).index in (None, index):
-            total += int(ws[:4].view(torch.int32).item())
+            total += _split_timeouts_of(ws)
     return total

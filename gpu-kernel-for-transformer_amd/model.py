@@ -152,6 +152,7 @@ class UserOptimizedTransformer(nn.Module):
         self._kv_cache_length = 0
         self._large_batch_chunk_size = self._shape_execution_plan.batch_chunk_size
         self._fused_stack_enabled = True
+        self._strict_handoff_checks = False
         # Recorded for the reference's toggles (TTB:379-406); see their methods.
         self._triton_fused_norm_enabled = True
         self._triton_fused_ffn_enabled = True
@@ -202,6 +203,15 @@ class UserOptimizedTransformer(nn.Module):
         paths compute the same math (FP16 operands, FP32 accumulation).
         """
         self._fused_stack_enabled = bool(enabled)
+
+    def enable_strict_handoff_checks(self, enabled: bool = True) -> None:
+        """Synchronise after each split-form whole-stack launch and raise if a K/V hand-off timed out.
+
+        A timed-out hand-off already turns the affected output rows into NaN;
+        this debug mode turns it into a RuntimeError at the call (one host
+        sync per forward).
+        """
+        self._strict_handoff_checks = bool(enabled)
 
     def enable_kv_cache(self, enabled: bool = True) -> None:
         """Incremental decoding over a per-layer FP16 KV cache, clearing any previous sequence (TTB:408-415).
@@ -402,7 +412,8 @@ class UserOptimizedTransformer(nn.Module):
         if self._uses_fused_stack(x) and (not masked or cfg.head_dim <= 64):
             wpack, ppack, affine_mask = self._fused_stack_parameters()
             return kernels.fused_forward_d128(x, wpack, ppack, cfg.num_heads, cfg.ffn_dim, len(self.layers), out=out,
-                                              affine_mask=affine_mask, token_valid=token_valid, causal=cfg.causal)
+                                              affine_mask=affine_mask, token_valid=token_valid, causal=cfg.causal,
+                                              strict=self._strict_handoff_checks)
 
         def attend(index: int, layer: TransformerBlockParameters, qkv: torch.Tensor) -> torch.Tensor:
             return kernels.attention(qkv, cfg.num_heads, key_valid=token_valid, causal=cfg.causal,

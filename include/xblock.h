@@ -20,7 +20,7 @@
 extern "C" {
 #endif
 
-#define XB_ABI_VERSION 1
+#define XB_ABI_VERSION 2
 
 /* Argument errors (negative); positive values are hipError_t codes. */
 #define XB_OK 0
@@ -158,6 +158,7 @@ int xb_attention_kv_cache(const void* qkv, const void* k_cache,
                           void* workspace, int64_t workspace_bytes,
                           void* stream);
 
+
 /* Fragment orders of xb_pack_linear_fragments. */
 #define XB_PACK_PERMUTED 0  /* k = 32*ks + 4*(l/16) + (m & 3) + 16*(m >> 2) */
 #define XB_PACK_NATURAL 1   /* k = 32*ks + 8*(l/16) + m                      */
@@ -208,25 +209,43 @@ int xb_fused_forward_d128(const float* x, float* y, const void* wpack,
                           int64_t affine_mask, const uint8_t* token_valid,
                           int32_t causal, void* stream);
 
+/* spin_limit / fault_flags of xb_fused_forward_d128_ws. */
+#define XB_SPLIT_SPINS_DEFAULT (-1)    /* the library's bound, about 30-40 ms      */
+#define XB_SPLIT_FAULT_NO_PUBLISH 1    /* test only: the first workgroup of each
+                                          sequence never signals its K/V, so every
+                                          wait of the second runs out             */
+
 /*
  * xb_fused_forward_d128 with a caller workspace that lets small batches use
  * two workgroups per sequence (tokens 0..63 and 64..127; the first hands each
  * layer's K and V of its tokens to the second through the workspace), which
  * doubles the CUs a small batch occupies (at most 80 sequences; 96 at
- * head_dim 16, 128 at head_dim 8).  Same results,
- * bit for bit, as xb_fused_forward_d128.
+ * head_dim 16, 128 at head_dim 8).  Same results, bit for bit, as
+ * xb_fused_forward_d128.
  *   xb_fused_forward_d128_workspace_bytes: bytes the split needs (0 = this
  *     shape runs one workgroup per sequence: head_dim above 64, causal = 0,
  *     seq_len <= 64 or a batch above those limits).
- *   workspace: 16-byte aligned, zero-filled before its first use; every call
- *     lowers the hand-off flags it raised, so the workspace is reused as is
- *     (hipGraph replays included).  Calls that overlap in time must not
- *     share one workspace.
- *     NULL, or a shape that needs none, runs xb_fused_forward_d128; fewer
- *     than the needed bytes give XB_ERR_WORKSPACE.  Its layout depends only
- *     on `layers`, so a workspace sized for a larger batch serves a smaller
- *     one (the size for the largest split batch serves every batch).  Its first 4
- *     bytes count hand-offs that timed out (0 when every call was correct).
+ *   workspace: 16-byte aligned, zero-filled before its first use, then
+ *     reused as it is (hipGraph replays included): each launch signals with
+ *     its own epoch (the workspace's launch generation plus one, advanced by
+ *     the launch's last workgroup), so nothing left by an earlier launch can
+ *     satisfy a later one.  Launches that overlap in time must not share a
+ *     workspace.  NULL, or a shape that needs none, runs
+ *     xb_fused_forward_d128; fewer than the needed bytes give
+ *     XB_ERR_WORKSPACE.  Its layout depends only on `layers`, so a workspace
+ *     sized for a larger batch serves a smaller one (the size for the
+ *     largest split batch serves every batch).  Its first 4 bytes (int32)
+ *     count hand-offs that timed out (0 when every call was correct); bytes
+ *     8..15 (uint64) count completed split launches.
+ *   spin_limit: sleeps (s_sleep 1 each) the second workgroup waits for a
+ *     layer's K/V before it gives up; XB_SPLIT_SPINS_DEFAULT for the
+ *     library's bound.  The two workgroups of a sequence run on one XCD with
+ *     the first dispatched first, and the first never waits, so a wait only
+ *     runs out when something else is broken.  A wait that runs out adds 1
+ *     to the timeout counter and makes that workgroup's output rows NaN (the
+ *     kernel still completes), so a failed hand-off can never pass for a
+ *     result.
+ *   fault_flags: 0, or XB_SPLIT_FAULT_NO_PUBLISH to exercise that path.
  * Replaces the same reference path as xb_fused_forward_d128.
  */
 int64_t xb_fused_forward_d128_workspace_bytes(int64_t batch, int32_t seq_len,
@@ -238,6 +257,7 @@ int xb_fused_forward_d128_ws(const float* x, float* y, const void* wpack,
                              int32_t layers, int64_t affine_mask,
                              const uint8_t* token_valid, int32_t causal,
                              void* workspace, int64_t workspace_bytes,
+                             int32_t spin_limit, int32_t fault_flags,
                              void* stream);
 
 #ifdef __cplusplus

@@ -166,9 +166,10 @@ def test_argument_errors_need_no_gpu(capi):
     assert lib.xb_residual_layernorm_masked(16, 16, 1, None, None, None, 16, 1, 4, 128, 1e-5, 0, None, 2, None) == -1
     assert lib.xb_residual_layernorm_masked(16, 16, 1, None, None, None, 16, 1, 0, 128, 1e-5, 0, None, 7, None) == 0
     # Fused d128 stack: which shapes split over two workgroups, and the workspace checks.
-    # Layout: timeout counter, flags of 128 sequences x layers, K/V slots from a 256-byte boundary.
+    # Layout: 256-byte header (timeout counter, finished blocks, generation), 64-bit flags of
+    # 128 sequences x layers, K/V slots from a 256-byte boundary.
     slot = 2 * 64 * 128 * 2
-    head = lambda layers: (4 * (1 + 128 * layers) + 255) // 256 * 256
+    head = lambda layers: (256 + 8 * 128 * layers + 255) // 256 * 256
     assert lib.xb_fused_forward_d128_workspace_bytes(64, 128, 4, 4, 1) == head(4) + 64 * 4 * slot
     assert lib.xb_fused_forward_d128_workspace_bytes(80, 65, 4, 2, 1) == head(2) + 80 * 2 * slot
     assert lib.xb_fused_forward_d128_workspace_bytes(81, 128, 4, 4, 1) == 0    # head_dim 32: no gain from here on
@@ -181,10 +182,11 @@ def test_argument_errors_need_no_gpu(capi):
     assert lib.xb_fused_forward_d128_workspace_bytes(64, 128, 1, 4, 1) == 0    # head_dim 128
     need = head(4) + 64 * 4 * slot
     ws_args = (16, 16, 16, 16, 64, 128, 4, 128, 4, -1, None, 1)
-    assert lib.xb_fused_forward_d128_ws(*ws_args, 16, need - 1, None) == -7
-    assert lib.xb_fused_forward_d128_ws(*ws_args, 24, need, None) == -5
-    assert lib.xb_fused_forward_d128_ws(16, 16, 16, 16, 64, 129, 4, 128, 4, -1, None, 1, 16, 1 << 30, None) == -4
-    assert lib.xb_fused_forward_d128_ws(16, 16, 16, 16, 0, 128, 4, 128, 4, -1, None, 1, None, 0, None) == 0
+    assert lib.xb_fused_forward_d128_ws(*ws_args, 16, need - 1, -1, 0, None) == -7
+    assert lib.xb_fused_forward_d128_ws(*ws_args, 24, need, -1, 0, None) == -5
+    assert lib.xb_fused_forward_d128_ws(*ws_args, 16, need, -1, 2, None) == -6    # unknown fault flag
+    assert lib.xb_fused_forward_d128_ws(16, 16, 16, 16, 64, 129, 4, 128, 4, -1, None, 1, 16, 1 << 30, -1, 0, None) == -4
+    assert lib.xb_fused_forward_d128_ws(16, 16, 16, 16, 0, 128, 4, 128, 4, -1, None, 1, None, 0, -1, 0, None) == 0
     for code in (0, -1, -2, -3, -4, -5, -6, -7):
         assert lib.xb_strerror(code)
     with pytest.raises(RuntimeError, match="xb_linear failed with code -4"):
