@@ -37,6 +37,7 @@ XB_MASK_SUM = 2
 XB_MASK_OUTPUT = 4
 XB_SPLIT_SPINS_DEFAULT = -1
 XB_SPLIT_FAULT_NO_PUBLISH = 1
+XB_DECODE_SCRATCH_BYTES = 32 << 20
 
 EXPORTED_SYMBOLS = (
     "xb_abi_version",
@@ -50,6 +51,7 @@ EXPORTED_SYMBOLS = (
     "xb_kv_cache_append",
     "xb_attention_kv_cache_workspace_bytes",
     "xb_attention_kv_cache",
+    "xb_attention_kv_cache_noalloc",
     "xb_pack_linear_fragments",
     "xb_fused_forward_d128",
     "xb_fused_forward_d128_workspace_bytes",
@@ -81,6 +83,10 @@ _SIGNATURES = {
     "xb_attention_kv_cache": (
         ctypes.c_int,
         [_vp, _vp, _vp, _vp, _i32, _i64, _i32, _i32, _i64, _i64, _f32, _vp, _i64, _vp],
+    ),
+    "xb_attention_kv_cache_noalloc": (
+        ctypes.c_int,
+        [_vp, _vp, _vp, _vp, _i32, _i64, _i32, _i32, _i64, _i64, _f32, _vp],
     ),
     "xb_pack_linear_fragments": (ctypes.c_int, [_vp, _vp, _i32, _i32, _i32, _f32, _vp]),
     "xb_fused_forward_d128": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i64, _vp, _i32, _vp]),

@@ -35,6 +35,8 @@
 // FP16); the decision is wave-uniform.  Only tiles that straddle the diagonal
 // pay for the mask.
 #include <algorithm>
+#include <atomic>
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -1033,5 +1035,58 @@ extern "C" int xb_attention_kv_cache(const void* qkv, const void* k_cache, const
                               if ((uintptr_t)workspace & 15u) return XB_ERR_MISALIGNED;
                               *ptr = workspace;
                               return XB_OK;
+                            });
+}
+
+// ---------------------------------------------------------------------------
+// No-allocation decode: the split partials live in `scratch`, a file-scope
+// device array (every GPU the library runs on holds its own copy, for the
+// life of the process).  Host code never passes `scratch` itself to a kernel
+// -- on the host that name is only a stand-in for the symbol -- but the
+// address hipGetSymbolAddress returns for it, looked up once per device with
+// that device current and kept in `g_scratch_ptr`.  The partials need no
+// clearing: every split writes its (o, offset, sum) slots before the combine
+// kernel, ordered after it on the same stream, reads them.
+static __device__ __align__(256) char scratch[XB_DECODE_SCRATCH_BYTES];
+
+constexpr int kMaxScratchDevices = 64;
+static std::atomic<void*> g_scratch_ptr[kMaxScratchDevices];
+static std::mutex g_scratch_mutex;
+
+// The current device's scratch address; the stream (NULL = the current
+// device's default stream) must belong to the current device.
+static int scratch_address(hipStream_t stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxScratchDevices) return XB_ERR_WRONG_DEVICE;
+  if (stream != nullptr) {
+    hipDevice_t stream_dev = -1;
+    e = hipStreamGetDevice(stream, &stream_dev);
+    if (e != hipSuccess) return (int)e;
+    if ((int)stream_dev != dev) return XB_ERR_WRONG_DEVICE;
+  }
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return (int)e;
+      if (p == nullptr) return (int)hipErrorInvalidSymbol;
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return XB_OK;
+}
+
+extern "C" int xb_attention_kv_cache_noalloc(const void* qkv, const void* k_cache, const void* v_cache, void* out,
+                                             int32_t batch, int64_t chunk, int32_t heads, int32_t head_dim,
+                                             int64_t start, int64_t capacity, float scale, void* stream) {
+  return attention_kv_cache(qkv, k_cache, v_cache, out, batch, chunk, heads, head_dim, start, capacity, scale, stream,
+                            [&](int64_t need, void** ptr) {
+                              if (need > XB_DECODE_SCRATCH_BYTES) return XB_ERR_SCRATCH_TOO_SMALL;
+                              return scratch_address(static_cast<hipStream_t>(stream), ptr);
                             });
 }

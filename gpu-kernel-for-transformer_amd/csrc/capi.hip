@@ -17,6 +17,9 @@ extern "C" const char* xb_strerror(int code) {
     case XB_ERR_MISALIGNED: return "xblock: a pointer is not 16-byte aligned";
     case XB_ERR_BAD_EPILOGUE: return "xblock: unknown GEMM epilogue, mask mode or flag";
     case XB_ERR_WORKSPACE: return "xblock: workspace smaller than the call needs";
+    case XB_ERR_WRONG_DEVICE: return "xblock: the stream does not belong to the current device";
+    case XB_ERR_SCRATCH_TOO_SMALL:
+      return "xblock: the call needs more than the static scratch (XB_DECODE_SCRATCH_BYTES); pass a workspace";
     default:
       if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
       return "xblock: unknown error";

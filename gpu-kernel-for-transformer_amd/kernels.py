@@ -347,12 +347,16 @@ def attention_kv_cache(
     scale: Optional[float] = None,
     out: Optional[torch.Tensor] = None,
     workspace: Optional[torch.Tensor] = None,
+    no_alloc: bool = False,
 ) -> torch.Tensor:
     """Causal attention of a chunk at positions start.. over the cached keys 0..start+chunk-1.
 
     Call after kv_cache_append for the same chunk (TTB:747-765).  `workspace`
     (uint8, at least kv_cache_workspace_bytes) is allocated here when not
-    given; decode chunks of up to 16 tokens need one.
+    given; decode chunks of up to 16 tokens need one.  no_alloc=True calls
+    xb_attention_kv_cache_noalloc instead, whose partials live in the
+    library's static per-GPU scratch (with `out` given, nothing is
+    allocated); calls that overlap in time on one GPU must not use it.
     """
     _require_device(qkv, "attention_kv_cache")
     batch, chunk, head_dim, capacity = _check_kv_cache(qkv, k_cache, v_cache, num_heads)
@@ -363,6 +367,15 @@ def attention_kv_cache(
     d_model = num_heads * head_dim
     if out is None:
         out = torch.empty((batch, chunk, d_model), device=qkv.device, dtype=torch.float16)
+    if no_alloc:
+        with torch.cuda.device(qkv.device):
+            check(
+                _launch(f"attention_kv_hd{head_dim}_noalloc", lambda: lib().xb_attention_kv_cache_noalloc(
+                    qkv.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(), batch, chunk, num_heads,
+                    head_dim, int(start), capacity, float(scale), stream_handle(qkv.device))),
+                "xb_attention_kv_cache_noalloc",
+            )
+        return out
     need = kv_cache_workspace_bytes(batch, chunk, num_heads, head_dim, start)
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty(need, device=qkv.device, dtype=torch.uint8)

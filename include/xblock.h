@@ -31,6 +31,8 @@ extern "C" {
 #define XB_ERR_MISALIGNED (-5)
 #define XB_ERR_BAD_EPILOGUE (-6)
 #define XB_ERR_WORKSPACE (-7)   /* workspace_bytes below what the call needs */
+#define XB_ERR_WRONG_DEVICE (-8) /* the stream is not on the current device   */
+#define XB_ERR_SCRATCH_TOO_SMALL (-9) /* more than the static scratch holds  */
 
 /* Element types of activations. */
 #define XB_F32 0
@@ -158,6 +160,27 @@ int xb_attention_kv_cache(const void* qkv, const void* k_cache,
                           void* workspace, int64_t workspace_bytes,
                           void* stream);
 
+/*
+ * xb_attention_kv_cache without a workspace argument, for callers that cannot
+ * allocate (code under hipGraph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  No counterpart in the reference.  A decode chunk's
+ * split partials go to a static device buffer of XB_DECODE_SCRATCH_BYTES
+ * that the library holds on each GPU it runs on until the process ends; the
+ * call allocates nothing.  A call needing more than that (batch * heads
+ * beyond about 7,900 at head_dim 64, 2,000 at head_dim 256) returns
+ * XB_ERR_SCRATCH_TOO_SMALL without launching; use xb_attention_kv_cache with
+ * a workspace then.  The stream must belong to the current device
+ * (XB_ERR_WRONG_DEVICE otherwise).  All calls on one GPU share its buffer:
+ * calls that overlap in time on one GPU (different streams, or concurrent
+ * graph replays) race and must not be issued.  Results equal
+ * xb_attention_kv_cache's bit for bit.
+ */
+#define XB_DECODE_SCRATCH_BYTES (32LL << 20)
+int xb_attention_kv_cache_noalloc(const void* qkv, const void* k_cache,
+                                  const void* v_cache, void* out,
+                                  int32_t batch, int64_t chunk, int32_t heads,
+                                  int32_t head_dim, int64_t start,
+                                  int64_t capacity, float scale, void* stream);
 
 /* Fragment orders of xb_pack_linear_fragments. */
 #define XB_PACK_PERMUTED 0  /* k = 32*ks + 4*(l/16) + (m & 3) + 16*(m >> 2) */

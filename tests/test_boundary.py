@@ -187,7 +187,11 @@ def test_argument_errors_need_no_gpu(capi):
     assert lib.xb_fused_forward_d128_ws(*ws_args, 16, need, -1, 2, None) == -6    # unknown fault flag
     assert lib.xb_fused_forward_d128_ws(16, 16, 16, 16, 64, 129, 4, 128, 4, -1, None, 1, 16, 1 << 30, -1, 0, None) == -4
     assert lib.xb_fused_forward_d128_ws(16, 16, 16, 16, 0, 128, 4, 128, 4, -1, None, 1, None, 0, -1, 0, None) == 0
-    for code in (0, -1, -2, -3, -4, -5, -6, -7):
+    # No-allocation decode: a call whose partials exceed the static scratch is refused before any launch
+    assert lib.xb_attention_kv_cache_noalloc(16, 16, 16, 16, 20000, 1, 16, 64, 100, 101, 0.1, None) == -9
+    assert lib.xb_attention_kv_cache_noalloc(None, 16, 16, 16, 1, 1, 2, 64, 100, 101, 0.1, None) == -1
+    assert lib.xb_attention_kv_cache_noalloc(16, 16, 16, 16, 1, 1, 2, 64, 100, 100, 0.1, None) == -2
+    for code in (0, -1, -2, -3, -4, -5, -6, -7, -8, -9):
         assert lib.xb_strerror(code)
     with pytest.raises(RuntimeError, match="xb_linear failed with code -4"):
         capi.check(-4, "xb_linear")
