@@ -9,15 +9,30 @@ checkpoint); input: x ~ N(0,1) from seed 1234+100000 (synthetic), as the
 reference's benchmark draws it (torch_transformer_benchmark.py:1478-1485).
 
 Printed as ONE JSON line with, besides the driver's fields:
-  roofline      the dominant kernel (largest share of step time), timed with
-                HIP events around each of its launches inside the timed steps
-                (on the launch stream), against its algorithmic bytes or FLOPs
-  cpu_baseline  the CPU FP32 oracle (restated BaselineTransformer) on a bounded
-                sample of the same workload, on this host's cores; its outputs
-                double as the accuracy check of the GPU output on that sample
-  per_config    tokens/s, ms and roofline fraction for all five BASELINE
-                configs, each with its accuracy result on a bounded sample
-Only one GPU is used; --gpus above 1 exits with an explanation.
+  roofline        the headline's dominant kernel (largest share of step time),
+                  timed with HIP events around each of its launches inside
+                  eager steps (on the launch stream), against its algorithmic
+                  bytes or FLOPs; `traffic` from rocprofv3 FETCH/WRITE_SIZE
+  forward_roofline  the whole forward against its own lower bound: max(FLOPs /
+                  MFMA peak, (x read + y written + weights) / HBM peak)
+  cpu_baseline    the CPU FP32 oracle (restated BaselineTransformer) on a
+                  bounded sample of the same workload, on all of this host's
+                  cores (len(os.sched_getaffinity(0)) threads)
+  accuracy        the reference's rule (TTB:1237-1304) on the GPU output against
+                  the oracle: whole batch for every config but cfg5, whose
+                  causal 4096-token prefix is checked on its first, middle and
+                  last sequences (all 32 with --full-accuracy); every config's
+                  whole output must also be finite (streamed_shape14.py:167-169)
+  per_config      all five BASELINE configs: tokens/s, ms, execution plan,
+                  dominant-kernel roofline, forward roofline, accuracy; cfg2
+                  also times the reference's own shape-6 form (chunks of 1024
+                  with a hipGraph per chunk shape, TTB:1740, :1826-1846)
+  decode          KV-cached single-token steps at cfg5's geometry
+A config whose device-memory estimate exceeds --memory-fraction of the GPU is
+skipped before anything is allocated, and an out-of-memory error skips it
+(the reference's SAFE_SKIP / SAFE_ABORT, streamed_shape14.py:197-222); for the
+headline workload both exit with status 3.  Only one GPU is used; --gpus
+above 1 exits with an explanation.
 """
 
 from __future__ import annotations
@@ -29,6 +44,7 @@ import statistics
 import sys
 import time
 from pathlib import Path
+from typing import Optional
 
 REPO = Path(__file__).resolve().parent
 sys.path.insert(0, str(REPO))
@@ -37,9 +53,12 @@ HBM_BYTES_PER_S = 8.0e12          # MI355X HBM3E peak
 FP16_MFMA_FLOPS = 2.5166e15       # MI355X dense FP16 MFMA peak (256 CU x 2.4 GHz x 4096)
 CONFIG_NAMES = {1: "cfg1", 6: "cfg2", 8: "cfg3", 11: "cfg4", 14: "cfg5"}
 CPU_SAMPLE_ROWS = {1: 64, 6: 256, 8: 16, 11: 64, 14: 1}
+LONG_PREFIX = 4096                # causal prefix checked for sequences longer than 8192
+EXIT_SKIPPED = 3                  # streamed_shape14.py:214, :222
+EXIT_ACCURACY = 2                 # torch_transformer_benchmark.py:1862-1865
 
 
-def parse_args():
+def parse_args(argv=None):
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
@@ -61,10 +80,15 @@ def parse_args():
                    help="run the headline with this batch instead of the shape's (the line then says so)")
     p.add_argument("--accuracy-trials", type=int, default=1,
                    help="accuracy samples: the timed input, then fresh inputs seeded 1234+t (TTB:1307-1372)")
+    p.add_argument("--full-accuracy", action="store_true", help="cfg5: check all 32 sequences' prefixes")
     p.add_argument("--strict-accuracy", action="store_true", help="exit with status 2 when an accuracy check fails")
-    args = p.parse_args()
+    p.add_argument("--memory-fraction", type=float, default=0.9,
+                   help="skip a config whose device-memory estimate exceeds this fraction of the GPU")
+    args = p.parse_args(argv)
     if args.steps <= 0 or args.warmup < 0 or args.rounds <= 0 or args.accuracy_trials <= 0 or args.batch < 0:
         p.error("steps, rounds and accuracy trials must be positive; warmup and batch non-negative")
+    if not 0 < args.memory_fraction <= 1:
+        p.error("--memory-fraction must be in (0, 1]")
     return args
 
 
@@ -73,13 +97,22 @@ def case_name(shape_id: int) -> str:
 
 
 def sample_rows(shape_id: int, config) -> int:
-    """Sequences in the bounded CPU-oracle sample of a workload."""
+    """Sequences per call of the bounded CPU-baseline timing sample."""
     if shape_id in CPU_SAMPLE_ROWS:
-        return CPU_SAMPLE_ROWS[shape_id]
+        return min(CPU_SAMPLE_ROWS[shape_id], config.batch_size)
     if config.seq_len > 8192:
         return 1
     budget = 8192 if config.d_model <= 256 else 2048  # tokens per oracle call
     return max(1, min(config.batch_size, budget // config.seq_len))
+
+
+def accuracy_rows(config, full: bool):
+    """Sequences whose output is checked against the oracle: all, or for long
+    sequences (causal prefix only) the first, middle and last."""
+    b = config.batch_size
+    if config.seq_len <= 8192 or full:
+        return list(range(b))
+    return sorted({0, b // 2, b - 1})
 
 
 def kernel_costs(name: str, config, rows: int):
@@ -89,7 +122,7 @@ def kernel_costs(name: str, config, rows: int):
     if name.startswith("layernorm"):
         return rows * 6 * d, 0.0
     if name.startswith("residual_layernorm"):
-        return rows * (10 if name.endswith("_final") else 12) * d, 0.0
+        return rows * (10 if "_final" in name else 12) * d, 0.0
     if name.startswith("attention"):
         return rows * 8 * d, 2.0 * b * d * s * (s + 1)
     if name in ("fused_forward_d128", "fused_forward_d128_split"):
@@ -103,16 +136,55 @@ def kernel_costs(name: str, config, rows: int):
         parts = name.split("_")
         n, k = int(parts[1][1:]), int(parts[2][1:])
         return rows * 2 * (n + k) + 2 * n * k, 2.0 * rows * n * k
-    raise KeyError(name)
+    return 0.0, 0.0
 
 
 def roofline_of(bytes_, flops, seconds):
     t_hbm, t_mfma = bytes_ / HBM_BYTES_PER_S, flops / FP16_MFMA_FLOPS
     if t_mfma > t_hbm:
         achieved = flops / seconds / 1e12
-        return {"bound": "mfma", "achieved": achieved, "peak": FP16_MFMA_FLOPS / 1e12, "unit": "TFLOP/s", "frac": achieved * 1e12 / FP16_MFMA_FLOPS}
+        return {"bound": "mfma", "achieved": achieved, "peak": FP16_MFMA_FLOPS / 1e12, "unit": "TFLOP/s",
+                "frac": achieved * 1e12 / FP16_MFMA_FLOPS}
     achieved = bytes_ / seconds / 1e9
-    return {"bound": "hbm", "achieved": achieved, "peak": HBM_BYTES_PER_S / 1e9, "unit": "GB/s", "frac": achieved * 1e9 / HBM_BYTES_PER_S}
+    return {"bound": "hbm", "achieved": achieved, "peak": HBM_BYTES_PER_S / 1e9, "unit": "GB/s",
+            "frac": achieved * 1e9 / HBM_BYTES_PER_S}
+
+
+def forward_lower_bound(config, flops: float):
+    """(bound, seconds) of the whole forward read once / computed once: x in, y out, weights once."""
+    tokens = config.batch_size * config.seq_len
+    d, f, layers = config.d_model, config.ffn_dim, config.num_layers
+    min_bytes = 8.0 * tokens * d + 2.0 * layers * (4 * d * d + 2 * d * f)
+    t_mfma, t_hbm = flops / FP16_MFMA_FLOPS, min_bytes / HBM_BYTES_PER_S
+    return ("mfma", t_mfma) if t_mfma >= t_hbm else ("hbm", t_hbm)
+
+
+def device_estimate_bytes(pkg, config) -> int:
+    """Device memory one config's leg needs: the forward working set (per-op
+    path, the larger) plus FP32 and FP16 weights and the output's clone."""
+    d, f, layers = config.d_model, config.ffn_dim, config.num_layers
+    cfg_mod = __import__(pkg.__name__ + ".config", fromlist=["forward_working_set_bytes"])
+    activations = cfg_mod.forward_working_set_bytes(config, config.batch_size, config.seq_len)
+    clone = 4 * config.batch_size * config.seq_len * d
+    weights = 8 * layers * (4 * d * d + 2 * d * f + 4 * d + f)
+    return activations + clone + weights
+
+
+def memory_preflight(estimate: int, free_bytes: int, total_bytes: int, fraction: float) -> Optional[str]:
+    """None if `estimate` fits min(free, fraction * total), else the SAFE_SKIP reason."""
+    budget = min(free_bytes, total_bytes * fraction)
+    if estimate <= budget:
+        return None
+    return (f"SAFE_SKIP: device-memory estimate {estimate / 2**30:.2f} GiB exceeds the budget "
+            f"{budget / 2**30:.2f} GiB (min of free memory and {fraction:.0%} of {total_bytes / 2**30:.2f} GiB); "
+            "no model or input was allocated")
+
+
+def nonfinite_count(out) -> int:
+    """Elements of the (whole) output that are NaN or Inf, counted on its device."""
+    import torch
+
+    return int((~torch.isfinite(out)).sum().item())
 
 
 def log(*a):
@@ -121,7 +193,7 @@ def log(*a):
 
 # Kernel symbol substring of each LaunchRecorder name (for counter CSVs).
 KERNEL_SYMBOLS = (("fused_forward_d128_split", "fused_split"), ("fused_forward_d128", "fused_stack"),
-                  ("attention", "attn_kernel"),
+                  ("attention", "attn_"),
                   ("gemm_", "gemm_"), ("residual_layernorm", "ln_"), ("layernorm", "ln_"))
 CALIBRATION_BYTES = 1 << 30
 
@@ -180,22 +252,46 @@ def measure_traffic(workload: int, dominant: str, batch: int = 0):
 
 DECODE_CONFIG = (32, 100000, 1024, 16, 1024, 2)   # cfg5's geometry; the cache holds seq_len tokens
 DECODE_SPARE = 16                                  # cache slots left for the decode steps
+DECODE_CHECK = (2, 4096)                           # (batch, cache capacity) of the oracle-checked decode
 
 
-def decode_leg(pkg, kernels, device, time_steps):
+def decode_leg(pkg, kernels, device, time_steps, threads):
     """KV-cached decoding at cfg5's geometry: B=32 caches of 99,984 tokens, one new token per step.
 
     A step is one forward of [32, 1, 1024] with the cache enabled; its cost is
     dominated by the split-key attention reading each layer's K/V cache
-    (4*B*S_k*D bytes per layer).  The first step's output is checked against
-    the uncached forward's row at the same position (the reference's rule,
-    computed here), i.e. the flash path's causal attention.
+    (4*B*S_k*D bytes per layer).  Correctness: the same decode path on a
+    4095-token prompt plus one step (B=2), against the CPU oracle's forward
+    over the 4096 tokens (the step's row); the oracle cannot run 100k-token
+    attention.  The long run's first step is also compared with the model's
+    own uncached forward (a consistency check, labelled as such).
     """
     import torch
+    from oracle.accuracy import compare_outputs
+    from oracle.baseline import BaselineTransformer, copy_model_weights
 
     cfg = pkg.TransformerConfig(*DECODE_CONFIG, True)
     torch.manual_seed(1234)
-    model = pkg.UserOptimizedTransformer(cfg).to(device).eval()
+    baseline = BaselineTransformer(cfg).eval()
+    model = pkg.UserOptimizedTransformer(cfg)
+    copy_model_weights(baseline, model)
+    model = model.to(device).eval()
+
+    # Oracle check on a cache the CPU can attend over.
+    b_chk, cap_chk = DECODE_CHECK
+    small = pkg.UserOptimizedTransformer(pkg.TransformerConfig(b_chk, cap_chk, 1024, 16, 1024, 2, True))
+    small.load_state_dict(model.state_dict())
+    small = small.to(device).eval()
+    g = torch.Generator(device=device).manual_seed(1234 + 300000)
+    x_chk = torch.randn(b_chk, cap_chk, 1024, generator=g, device=device)
+    small.enable_kv_cache(True)
+    with torch.inference_mode():
+        small(x_chk[:, : cap_chk - 1])
+        step_out = small(x_chk[:, cap_chk - 1:]).cpu()
+        ref = baseline(x_chk.cpu())[:, cap_chk - 1:]
+    oracle_check = compare_outputs(ref, step_out)
+    del small, x_chk
+
     prompt = cfg.seq_len - DECODE_SPARE
     g = torch.Generator(device=device).manual_seed(1234 + 200000)
     x_all = torch.randn(cfg.batch_size, prompt + 1, cfg.d_model, generator=g, device=device)
@@ -215,8 +311,7 @@ def decode_leg(pkg, kernels, device, time_steps):
         model.enable_kv_cache(False)
         full = model(x_all)[:, prompt:]
         torch.cuda.synchronize()
-    diff = (first - full).abs()
-    failed = int(((diff > 2e-3) & (diff > 0.02 * full.abs())).sum().item()) + int((~torch.isfinite(first)).sum().item())
+    consistency = compare_outputs(full.cpu(), first.cpu())
     per = {}
     for name, durs in rec.durations_ms().items():
         per[name] = {"avg_us": round(statistics.fmean(durs) * 1e3, 2), "per_step": len(durs) // steps}
@@ -225,7 +320,12 @@ def decode_leg(pkg, kernels, device, time_steps):
         "workload": f"cfg5 geometry decode: B={cfg.batch_size}, cache {prompt}..{length} tokens, D={cfg.d_model}, "
                     f"H={cfg.num_heads}, L={cfg.num_layers}, one token per sequence per step",
         "ms_per_step": ms, "tokens_per_s": cfg.batch_size / (ms / 1e3),
-        "check_vs_uncached_forward": {"failed": failed, "total": first.numel(), "max_abs": float(diff.max().item())},
+        "check_vs_oracle": {"case": f"B={b_chk}, {cap_chk - 1}-token prompt + 1 decode step, CPU FP32 oracle "
+                                    f"on {threads} threads", "passed": oracle_check.passed,
+                            "failed": oracle_check.failed_elements, "total": oracle_check.total_elements,
+                            "max_abs": oracle_check.max_abs_error},
+        "consistency_vs_uncached_forward": {"failed": consistency.failed_elements, "total": consistency.total_elements,
+                                            "max_abs": consistency.max_abs_error},
         "kernels": per,
     }
     if attn is not None:
@@ -235,14 +335,15 @@ def decode_leg(pkg, kernels, device, time_steps):
         out["roofline"] = {"kernel": attn, "bound": "hbm", "achieved": by / sec / 1e9, "peak": HBM_BYTES_PER_S / 1e9,
                            "unit": "GB/s", "frac": by / sec / HBM_BYTES_PER_S, "bytes_per_launch": by}
         log(f"[bench] decode: {ms:.3f} ms/step, {out['tokens_per_s']:.4g} tokens/s; {attn} {per[attn]['avg_us']:.1f} us "
-            f"= {by / sec / 1e9:.0f} GB/s ({by / sec / HBM_BYTES_PER_S * 100:.1f}% of HBM); check failed={failed}")
-    del model, x_all
+            f"= {by / sec / 1e9:.0f} GB/s ({by / sec / HBM_BYTES_PER_S * 100:.1f}% of HBM); "
+            f"oracle check {oracle_check.summary()}")
+    del model, x_all, baseline
     torch.cuda.empty_cache()
     return out
 
 
-def main() -> int:
-    args = parse_args()
+def main(argv=None) -> int:
+    args = parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X only: this build has no multi-GPU path "
               "(the batch shards with no exchange step; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
@@ -251,9 +352,12 @@ def main() -> int:
     import torch
     import __graft_entry__ as entry
 
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
     pkg = entry.load_package()
     kernels = __import__(pkg.__name__ + ".kernels", fromlist=["LaunchRecorder"])
     graphs = __import__(pkg.__name__ + ".graph_runner", fromlist=["FixedInputCUDAGraph"])
+    chunking = __import__(pkg.__name__ + ".batch_chunk_runner", fromlist=["BatchChunkedTransformer"])
     if not pkg.XBLOCK_AVAILABLE:
         raise RuntimeError(f"libxblock.so unavailable: {pkg.XBLOCK_LOAD_ERROR}")
     device = torch.device("cuda:0")
@@ -286,6 +390,20 @@ def main() -> int:
         wall = time.perf_counter() - t0
         return start.elapsed_time(end) / steps, wall
 
+    def check_rows(baseline, config, out, x, rows):
+        """The rule on the given sequences, in groups that bound host memory."""
+        from oracle.accuracy import compare_outputs
+
+        prefix = LONG_PREFIX if config.seq_len > 8192 else config.seq_len
+        per_group = max(1, (1 << 21) // (prefix * config.d_model))
+        results = []
+        for i in range(0, len(rows), per_group):
+            idx = torch.tensor(rows[i:i + per_group], device=out.device)
+            with torch.inference_mode():
+                ref = baseline(x[:, :prefix].index_select(0, idx).float().cpu().contiguous())
+            results.append(compare_outputs(ref, out[:, :prefix].index_select(0, idx).cpu()))
+        return results
+
     def extra_trials(baseline, model, config, rows, trials):
         """Accuracy of fresh inputs seeded 1234+t, t = 1..trials-1, on `rows` sequences."""
         from oracle.accuracy import compare_outputs
@@ -297,24 +415,21 @@ def main() -> int:
             with torch.inference_mode():
                 out_t = model(xt)
                 if config.seq_len > 8192:  # long context: causal prefix only
-                    xt, out_t = xt[:, :4096], out_t[:, :4096]
+                    xt, out_t = xt[:, :LONG_PREFIX], out_t[:, :LONG_PREFIX]
                 ref_t = baseline(xt.float().cpu().contiguous())
             results.append(compare_outputs(ref_t, out_t.cpu()))
         return results
 
-    def cpu_leg(baseline, config, gpu_out, x_gpu, budget_s, rows_per_call):
-        """Oracle on the host cores over a bounded slice; returns rate and accuracy."""
-        from oracle.accuracy import compare_outputs
-
-        threads = torch.get_num_threads()
+    def cpu_leg(baseline, config, x_gpu, budget_s, rows_per_call):
+        """The oracle on the host cores over a bounded slice: tokens/s."""
         x_cpu = x_gpu[:rows_per_call].float().cpu()
         prefix = None
         if config.seq_len > 8192:  # long context: causal prefix only
-            prefix = 4096
+            prefix = LONG_PREFIX
             x_cpu = x_gpu[:rows_per_call, :prefix].float().cpu()
         with torch.inference_mode():
             t0 = time.perf_counter()
-            ref = baseline(x_cpu)
+            baseline(x_cpu)
             first = time.perf_counter() - t0
             calls, elapsed = 1, first
             while elapsed < budget_s * 0.5 and elapsed + first < budget_s:
@@ -323,20 +438,35 @@ def main() -> int:
                 elapsed += time.perf_counter() - t1
                 calls += 1
         tokens = calls * x_cpu.shape[0] * x_cpu.shape[1]
-        cand = gpu_out[:rows_per_call] if prefix is None else gpu_out[:rows_per_call, :prefix]
-        acc = compare_outputs(ref, cand.cpu())
         sample = f"{x_cpu.shape[0]} x {x_cpu.shape[1]} tokens per call, {calls} calls" + (
             f" (causal prefix {prefix} of S={config.seq_len})" if prefix else "")
-        return {"value": tokens / elapsed, "unit": "tokens/s", "cores": threads, "kind": "port", "sample": sample}, acc
+        return {"value": tokens / elapsed, "unit": "tokens/s", "cores": threads, "kind": "port", "sample": sample}
+
+    def kernel_profile(model, x, config, tokens, reps):
+        with torch.inference_mode(), kernels.LaunchRecorder() as rec:
+            for _ in range(reps):
+                model(x)
+        torch.cuda.synchronize()
+        per = {}
+        for kname, durs in rec.durations_ms().items():
+            avg = statistics.fmean(durs)
+            b_, f_ = kernel_costs(kname, config, tokens)
+            per[kname] = {"avg_ms": avg, "launches_per_step": len(durs) // reps,
+                          "share_ms": avg * len(durs) / reps, **roofline_of(max(b_, 1.0), f_, avg / 1e3),
+                          "bytes_per_launch": b_, "flops_per_launch": f_}
+        dominant = max(per, key=lambda k: per[k]["share_ms"])
+        return per, dominant
 
     if args.decode_only:
-        print(json.dumps({"decode": decode_leg(pkg, kernels, device, time_steps)}), flush=True)
+        print(json.dumps({"decode": decode_leg(pkg, kernels, device, time_steps, threads)}), flush=True)
         return 0
 
     results = {}
-    order = [args.workload] + ([] if (args.no_per_config or args.profile_only) else [i for i in CONFIG_NAMES if i != args.workload])
+    order = [args.workload] + ([] if (args.no_per_config or args.profile_only)
+                               else [i for i in CONFIG_NAMES if i != args.workload])
     headline = None
     accuracy_failed = False
+    free_bytes, total_bytes = torch.cuda.mem_get_info(device)
     for shape_id in order:
         config = pkg.OFFICIAL_BENCHMARK_SHAPES[shape_id]
         name = case_name(shape_id)
@@ -347,106 +477,39 @@ def main() -> int:
             config = dataclasses.replace(config, batch_size=args.batch)
             name = f"{name}-b{args.batch}"
         log(f"[bench] {name} (official shape {shape_id}): {config}")
-        baseline, model = build(config)
-        x = make_input(config, 1234 + 100000)
-        tokens = config.batch_size * config.seq_len
-        big = config.seq_len > 8192
-        if big:
-            steps, warmup = (max(1, min(args.steps, 3)), 1) if is_head else (2, 1)
-        else:
-            # Non-headline small configs: 20 warmups, 3 rounds of 100, median
-            # (the repeat counts the reference's harness suggests; a 20-step
-            # window right after the CPU leg still runs on a ramping clock).
-            steps, warmup = (args.steps, args.warmup) if is_head else (100, 20)
-        with torch.inference_mode():
-            if big or tokens >= 1_000_000:
-                run = lambda: model(x)  # noqa: E731  (launch-overhead-free at this size)
-                mode = "eager"
-            else:
-                # The reference harness's choice (cuda_graph_runner.maybe_cuda_graph):
-                # replay with the output clone, or eager for a one-kernel forward.
-                runner, graphed, status = graphs.maybe_cuda_graph(model, x, None, enabled=True)
-                run = lambda: runner(x)  # noqa: E731
-                mode = "hipGraph replay" if graphed else f"eager: {status}"
-            if big or (is_head and args.rounds == 1):
-                ms, wall = time_steps(run, steps, warmup)
-            elif is_head:
-                rounds = [time_steps(run, steps, warmup if r == 0 else 0) for r in range(args.rounds)]
-                ms, wall = statistics.median(r[0] for r in rounds), sum(r[1] for r in rounds)
-            else:
-                rounds = [time_steps(run, steps, warmup if r == 0 else 0) for r in range(3)]
-                ms, wall = statistics.median(r[0] for r in rounds), sum(r[1] for r in rounds)
-            out = model(x)
-            torch.cuda.synchronize()
-        entry_ = {
-            "workload": name, "official_shape": shape_id, "tokens_per_s": tokens / (ms / 1e3), "ms": ms,
-            "mode": mode, "steps": steps,
-        }
-        fl, by = pkg.forward_flops(config), pkg.forward_bytes(config)
-        t_bound = max(fl / FP16_MFMA_FLOPS, by / HBM_BYTES_PER_S)
-        entry_["bound"] = "mfma" if fl / FP16_MFMA_FLOPS > by / HBM_BYTES_PER_S else "hbm"
-        entry_["roofline_frac"] = t_bound / (ms / 1e3)
-        # Against the fully fused lower bound: read x, write y, weights once.
-        by_min = 8.0 * tokens * config.d_model + 2.0 * config.num_layers * (
-            4 * config.d_model ** 2 + 2 * config.d_model * config.ffn_dim)
-        t_min = max(fl / FP16_MFMA_FLOPS, by_min / HBM_BYTES_PER_S)
-        entry_["bound_min"] = "mfma" if fl / FP16_MFMA_FLOPS > by_min / HBM_BYTES_PER_S else "hbm"
-        entry_["roofline_frac_min"] = t_min / (ms / 1e3)
-        log(f"[bench] {name}: {ms:.3f} ms/step, {entry_['tokens_per_s']:.4g} tokens/s ({mode}), roofline frac "
-            f"{entry_['roofline_frac']:.3f} of the kernel pipeline's {entry_['bound']} bound, "
-            f"{entry_['roofline_frac_min']:.3f} of the fused lower bound ({entry_['bound_min']})")
-
-        if is_head:
-            headline = dict(entry_, config=config, wall=wall)
-            if not args.profile_only:
-                # Per-kernel durations with HIP events inside timed eager steps.
-                with torch.inference_mode(), kernels.LaunchRecorder() as rec:
-                    for _ in range(max(2, min(steps, 5))):
-                        model(x)
-                torch.cuda.synchronize()
-                per = {}
-                for kname, durs in rec.durations_ms().items():
-                    avg = statistics.fmean(durs)
-                    b_, f_ = kernel_costs(kname, config, tokens)
-                    per[kname] = {"avg_ms": avg, "launches_per_step": len(durs) // max(2, min(steps, 5)),
-                                  "share_ms": avg * len(durs) / max(2, min(steps, 5)), **roofline_of(b_, f_, avg / 1e3),
-                                  "bytes_per_launch": b_, "flops_per_launch": f_}
-                dominant = max(per, key=lambda k: per[k]["share_ms"])
-                headline["kernels"] = per
-                headline["dominant"] = dominant
-                for kname, v in sorted(per.items(), key=lambda kv: -kv[1]["share_ms"]):
-                    log(f"[bench]   {kname:28s} {v['avg_ms']*1e3:9.1f} us x{v['launches_per_step']} "
-                        f"{v['achieved']:9.1f} {v['unit']} ({v['frac']*100:5.1f}% {v['bound']})")
-
-        if not args.profile_only:
-            if args.no_cpu_baseline and not is_head:
-                pass
-            else:
-                rows = sample_rows(shape_id, config)
-                budget = args.cpu_seconds if is_head else min(args.cpu_seconds, 5.0)
-                if args.no_cpu_baseline:
-                    budget = 0.0
-                cpu, acc = cpu_leg(baseline, config, out, x, budget, rows)
-                checks = [acc] + (extra_trials(baseline, model, config, rows, args.accuracy_trials) if is_head else [])
-                entry_["accuracy"] = {"failed": sum(c.failed_elements for c in checks),
-                                      "total": sum(c.total_elements for c in checks),
-                                      "max_abs": max(c.max_abs_error for c in checks),
-                                      "passed": all(c.passed for c in checks), "trials": len(checks)}
-                accuracy_failed |= not entry_["accuracy"]["passed"]
-                if len(checks) > 1:
-                    log(f"[bench] {name}: {len(checks)} accuracy trials: " + "; ".join(c.summary() for c in checks))
-                entry_["cpu_baseline_tokens_per_s"] = cpu["value"]
-                log(f"[bench] {name}: accuracy {acc.summary()}; CPU FP32 oracle {cpu['value']:.4g} tokens/s on {cpu['cores']} threads ({cpu['sample']})")
-                if is_head:
-                    headline["cpu_baseline"] = cpu
-                    headline["accuracy"] = entry_["accuracy"]
+        estimate = device_estimate_bytes(pkg, config)
+        free_bytes, _ = torch.cuda.mem_get_info(device)
+        skip = memory_preflight(estimate, free_bytes, total_bytes, args.memory_fraction)
+        if skip is not None:
+            log(f"[bench] {name}: {skip}")
+            if is_head:
+                print(skip, flush=True)
+                return EXIT_SKIPPED
+            results[name] = {"workload": name, "official_shape": shape_id, "status": "SKIP", "reason": skip}
+            continue
+        try:
+            entry_, head_extra = run_config(
+                args, pkg, config, shape_id, name, is_head, build, make_input, time_steps, check_rows,
+                extra_trials, cpu_leg, kernel_profile, graphs, chunking)
+        except torch.cuda.OutOfMemoryError as error:
+            torch.cuda.empty_cache()
+            reason = f"SAFE_ABORT: out of device memory: {str(error).splitlines()[0]}"
+            log(f"[bench] {name}: {reason}")
+            if is_head:
+                print(reason, flush=True)
+                return EXIT_SKIPPED
+            results[name] = {"workload": name, "official_shape": shape_id, "status": "SKIP", "reason": reason}
+            continue
+        accuracy_failed |= not entry_.get("accuracy", {}).get("passed", True)
         results[name] = entry_
-        del baseline, model, x, out
+        if is_head:
+            headline = dict(entry_, config=config, **head_extra)
         torch.cuda.empty_cache()
 
     decode = None
     if not (args.no_per_config or args.profile_only or args.no_decode):
-        decode = decode_leg(pkg, kernels, device, time_steps)
+        decode = decode_leg(pkg, kernels, device, time_steps, threads)
+        accuracy_failed |= not decode["check_vs_oracle"]["passed"]
 
     if args.profile_only and args.copy_calibration:
         # A plain streaming copy of known size: reads and writes exactly
@@ -478,42 +541,145 @@ def main() -> int:
                         + (f" at batch {cfg.batch_size}" if args.batch else ""),
             "batch": cfg.batch_size, "seq_len": cfg.seq_len, "d_model": cfg.d_model, "heads": cfg.num_heads,
             "ffn_dim": cfg.ffn_dim, "layers": cfg.num_layers, "mode": headline["mode"],
+            "plan": headline["plan"],
         },
-        "roofline_frac_forward": headline["roofline_frac"],
-        "bound_forward": headline["bound"],
-        "roofline_frac_forward_min": headline["roofline_frac_min"],
-        "bound_forward_min": headline["bound_min"],
     }
-    if "dominant" in headline:
-        k = headline["kernels"][headline["dominant"]]
-        line["roofline"] = {
-            "kernel": headline["dominant"], "bound": k["bound"], "achieved": k["achieved"], "peak": k["peak"],
-            "unit": k["unit"], "frac": k["frac"], "traffic": None, "avg_us": k["avg_ms"] * 1e3,
-            "bytes_per_launch": k["bytes_per_launch"], "flops_per_launch": k["flops_per_launch"],
-        }
-        line["kernels"] = {n: {"avg_us": round(v["avg_ms"] * 1e3, 2), "per_step": v["launches_per_step"],
-                               "frac": round(v["frac"], 4), "bound": v["bound"]} for n, v in headline["kernels"].items()}
-    if "dominant" in headline and not args.no_traffic:
-        log(f"[bench] HBM traffic of {headline['dominant']}: two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE)")
-        traffic, detail = measure_traffic(args.workload, headline["dominant"], args.batch)
+    if "roofline" in headline:
+        line["roofline"] = dict(headline["roofline"], traffic=None)
+        line["kernels"] = headline["kernels"]
+    line["forward_roofline"] = headline["forward_roofline"]
+    line["pipeline_bytes_frac"] = headline["pipeline_bytes_frac"]
+    if "roofline" in headline and not args.no_traffic and not args.profile_only:
+        dominant = headline["roofline"]["kernel"]
+        log(f"[bench] HBM traffic of {dominant}: two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE)")
+        traffic, detail = measure_traffic(args.workload, dominant, args.batch)
         line["roofline"]["traffic"] = traffic
         line["roofline"]["traffic_detail"] = detail
         if traffic is not None:
-            log(f"[bench] traffic {traffic / 1e9:.4f} GB per launch vs algorithmic {line['roofline']['bytes_per_launch'] / 1e9:.4f} GB")
+            log(f"[bench] traffic {traffic / 1e9:.4f} GB per launch vs algorithmic "
+                f"{line['roofline']['bytes_per_launch'] / 1e9:.4f} GB")
         else:
             log(f"[bench] traffic unavailable: {detail}")
     if "cpu_baseline" in headline:
         line["cpu_baseline"] = headline["cpu_baseline"]
+    if "accuracy" in headline:
         line["accuracy"] = headline["accuracy"]
     if decode is not None:
         line["decode"] = decode
     if len(results) > 1:
-        line["per_config"] = {n: {k: (round(v, 6) if isinstance(v, float) else v) for k, v in r.items()} for n, r in results.items()}
+        line["per_config"] = {n: {k: v for k, v in r.items() if k not in ("kernels",)} for n, r in results.items()}
     print(json.dumps(line), flush=True)
     if args.strict_accuracy and accuracy_failed:
         log("[bench] accuracy check FAILED")
-        return 2
+        return EXIT_ACCURACY
     return 0
+
+
+def run_config(args, pkg, config, shape_id, name, is_head, build, make_input, time_steps, check_rows,
+               extra_trials, cpu_leg, kernel_profile, graphs, chunking):
+    """Time one config, profile its kernels, check it; returns (per-config entry, headline extras)."""
+    import torch
+
+    baseline, model = build(config)
+    x = make_input(config, 1234 + 100000)
+    tokens = config.batch_size * config.seq_len
+    big = config.seq_len > 8192
+    if big:
+        steps, warmup = (max(1, min(args.steps, 3)), 1) if is_head else (2, 1)
+    else:
+        # Non-headline small configs: 20 warmups, 3 rounds of 100, median
+        # (the repeat counts the reference's harness suggests).
+        steps, warmup = (args.steps, args.warmup) if is_head else (100, 20)
+    plan = model.execution_plan(config.batch_size, config.seq_len)
+    with torch.inference_mode():
+        if big or tokens >= 1_000_000:
+            run = lambda: model(x)  # noqa: E731  (launch-overhead-free at this size)
+            mode = "eager"
+        else:
+            # The reference harness's choice (cuda_graph_runner.maybe_cuda_graph):
+            # replay with the output clone, or eager for a one-kernel forward.
+            runner, graphed, status = graphs.maybe_cuda_graph(model, x, None, enabled=True)
+            run = lambda: runner(x)  # noqa: E731
+            mode = "hipGraph replay" if graphed else f"eager: {status}"
+        if big or (is_head and args.rounds == 1):
+            ms, wall = time_steps(run, steps, warmup)
+        else:
+            n_rounds = args.rounds if is_head else 3
+            rounds = [time_steps(run, steps, warmup if r == 0 else 0) for r in range(n_rounds)]
+            ms, wall = statistics.median(r[0] for r in rounds), sum(r[1] for r in rounds)
+        out = model(x)
+        torch.cuda.synchronize()
+    entry_ = {"workload": name, "official_shape": shape_id, "status": "PASS", "tokens_per_s": tokens / (ms / 1e3),
+              "ms": ms, "mode": mode, "steps": steps, "plan": plan.describe()}
+    flops = pkg.forward_flops(config)
+    bound, t_bound = forward_lower_bound(config, flops)
+    entry_["forward_roofline"] = {"bound": bound, "frac": t_bound / (ms / 1e3),
+                                  "note": "whole forward vs max(FLOPs/MFMA peak, (x+y+weights)/HBM peak)"}
+    pipe = pkg.forward_bytes(config) / HBM_BYTES_PER_S
+    entry_["pipeline_bytes_frac"] = {"frac": pipe / (ms / 1e3),
+                                     "note": "unfused kernel pipeline's bytes / HBM peak / step time; "
+                                             "not a roofline (a fused kernel moves fewer bytes, so it can exceed 1)"}
+    head_extra = {}
+    if not args.profile_only:
+        reps = 1 if big else max(2, min(steps, 5))
+        per, dominant = kernel_profile(model, x, config, tokens, reps)
+        k = per[dominant]
+        entry_["roofline"] = {"kernel": dominant, "bound": k["bound"], "achieved": k["achieved"], "peak": k["peak"],
+                              "unit": k["unit"], "frac": k["frac"], "avg_us": k["avg_ms"] * 1e3,
+                              "share_of_step": k["share_ms"] / ms, "bytes_per_launch": k["bytes_per_launch"],
+                              "flops_per_launch": k["flops_per_launch"]}
+        entry_["kernels"] = {n: {"avg_us": round(v["avg_ms"] * 1e3, 2), "per_step": v["launches_per_step"],
+                                 "frac": round(v["frac"], 4), "bound": v["bound"]} for n, v in per.items()}
+        head_extra["kernels"] = entry_["kernels"]
+        for kname, v in sorted(per.items(), key=lambda kv: -kv[1]["share_ms"]):
+            log(f"[bench]   {kname:28s} {v['avg_ms'] * 1e3:9.1f} us x{v['launches_per_step']} "
+                f"{v['achieved']:9.1f} {v['unit']} ({v['frac'] * 100:5.1f}% {v['bound']})")
+    log(f"[bench] {name}: {ms:.3f} ms/step, {entry_['tokens_per_s']:.4g} tokens/s ({mode}); plan {plan.describe()}; "
+        f"forward {entry_['forward_roofline']['frac']:.3f} of its {bound} lower bound"
+        + (f"; dominant {entry_['roofline']['kernel']} at {entry_['roofline']['frac']:.3f} of "
+           f"{entry_['roofline']['bound']} peak" if "roofline" in entry_ else ""))
+
+    if not args.profile_only:
+        bad = nonfinite_count(out)
+        rows = accuracy_rows(config, args.full_accuracy)
+        checks = check_rows(baseline, config, out, x, rows)
+        if is_head:
+            checks += extra_trials(baseline, model, config, min(config.batch_size, sample_rows(shape_id, config)),
+                                   args.accuracy_trials)
+        passed = all(c.passed for c in checks) and bad == 0
+        entry_["accuracy"] = {
+            "passed": passed, "failed": sum(c.failed_elements for c in checks),
+            "total": sum(c.total_elements for c in checks), "max_abs": max(c.max_abs_error for c in checks),
+            "sequences_checked": len(rows), "trials": 1 + (args.accuracy_trials - 1 if is_head else 0),
+            "nonfinite_in_whole_output": bad,
+            "prefix": LONG_PREFIX if config.seq_len > 8192 else None,
+        }
+        if not passed:
+            entry_["status"] = "FAIL"
+        log(f"[bench] {name}: accuracy on {len(rows)} sequences: failed {entry_['accuracy']['failed']}/"
+            f"{entry_['accuracy']['total']}, max_abs {entry_['accuracy']['max_abs']:.3g}; non-finite in the whole "
+            f"output: {bad}")
+        if not args.no_cpu_baseline or is_head:
+            budget = 0.0 if args.no_cpu_baseline else (args.cpu_seconds if is_head else min(args.cpu_seconds, 5.0))
+            cpu = cpu_leg(baseline, config, x, budget, sample_rows(shape_id, config))
+            entry_["cpu_baseline_tokens_per_s"] = cpu["value"]
+            log(f"[bench] {name}: CPU FP32 oracle {cpu['value']:.4g} tokens/s on {cpu['cores']} threads "
+                f"({cpu['sample']})")
+            if is_head:
+                head_extra["cpu_baseline"] = cpu
+    if shape_id == 6 and not args.profile_only and not args.batch:
+        # The reference's own shape-6 form: chunks of 1024 with a hipGraph per chunk shape.
+        chunked = chunking.BatchChunkedTransformer(model, 1024, all_tokens_valid=True, use_cuda_graphs=True)
+        with torch.inference_mode():
+            c_ms, _ = time_steps(lambda: chunked(x), 10, 2)
+            same = bool(torch.equal(chunked(x), out))
+        entry_["reference_form_chunk1024_graphs"] = {
+            "ms": c_ms, "tokens_per_s": tokens / (c_ms / 1e3), "equal_to_unchunked": same,
+            "status": chunked.graph_status}
+        log(f"[bench] {name}: chunk-1024 per-chunk graphs {c_ms:.3f} ms ({chunked.graph_status}); bitwise equal: {same}")
+        del chunked
+    del baseline, model, x, out
+    return entry_, head_extra
 
 
 if __name__ == "__main__":

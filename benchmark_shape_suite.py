@@ -11,13 +11,16 @@ ends as
   PASS   the case ran and every accuracy trial met the reference's rule
   PROXY  shape 14 on fewer than its 32 sequences (--shape14-samples); otherwise
          as PASS
-  SKIP   the preflight estimate does not fit (--force-oversized runs it anyway)
+  SKIP   the preflight estimate does not fit (--force-oversized runs it anyway),
+         or bench.py itself skipped it (status 3: its own memory preflight or
+         an out-of-memory error, the reference's SAFE_SKIP / SAFE_ABORT)
   FAIL   non-zero exit (an accuracy failure exits with 2), a time-out, or no
          result line
 
-and the summary gives tokens/s, ms per forward, the bound (HBM or FP16 MFMA)
-and the fraction of that roofline reached, with the accuracy counts, plus their
-geometric mean; --json writes the same as a file.  Exit status: 1 if a case
+and the summary gives tokens/s, ms per forward, the dominant kernel's bound
+(HBM or FP16 MFMA) and the fraction of that roofline it reached, the whole
+forward's fraction of its lower bound, the accuracy counts, and geometric
+means; --json writes the same as a file.  Exit status: 1 if a case
 FAILed, or with --strict if one was SKIPped or PROXY; else 0.
 
 Differences from the reference's runner: shape 14 runs at the real S=100000
@@ -61,6 +64,7 @@ class CaseResult:
     bound: Optional[str] = None
     roofline_frac: Optional[float] = None
     bound_min: Optional[str] = None
+    kernel: Optional[str] = None
     roofline_frac_min: Optional[float] = None
     accuracy_failed: Optional[int] = None
     accuracy_total: Optional[int] = None
@@ -196,10 +200,13 @@ def run_case(shape_id: int, config, args: argparse.Namespace, device_bytes: Opti
         result.line = line
         result.tokens_per_s = line.get("value")
         result.ms = line.get("ms_per_step")
-        result.roofline_frac = line.get("roofline_frac_forward")
-        result.bound = line.get("bound_forward")
-        result.roofline_frac_min = line.get("roofline_frac_forward_min")
-        result.bound_min = line.get("bound_forward_min")
+        kernel = line.get("roofline") or {}
+        forward = line.get("forward_roofline") or {}
+        result.roofline_frac = kernel.get("frac")
+        result.bound = kernel.get("bound")
+        result.kernel = kernel.get("kernel")
+        result.roofline_frac_min = forward.get("frac")
+        result.bound_min = forward.get("bound")
         accuracy = line.get("accuracy") or {}
         result.accuracy_failed = accuracy.get("failed")
         result.accuracy_total = accuracy.get("total")
@@ -207,6 +214,10 @@ def run_case(shape_id: int, config, args: argparse.Namespace, device_bytes: Opti
         result.cpu_tokens_per_s = (line.get("cpu_baseline") or {}).get("value")
     if status == 124:
         result.reason = f"timed out after {args.case_timeout:.0f} s"
+    elif status == 3:  # bench.py's SAFE_SKIP (preflight) or SAFE_ABORT (out of memory)
+        result.status = "SKIP"
+        result.reason = next((t.strip() for t in stdout.splitlines() if t.startswith("SAFE_")),
+                             "skipped by the benchmark (status 3)")
     elif status == 2 and line is not None:
         result.reason = "accuracy check failed"
     elif status != 0:
@@ -232,9 +243,9 @@ def geometric_mean(values: Sequence[float]) -> Optional[float]:
 
 def summary_lines(results: Sequence[CaseResult]) -> List[str]:
     out = ["=== Official shape-suite summary ===",
-           "roofline: fraction of the bound of the FP32-residual kernel pipeline's algorithmic bytes/FLOPs;",
-           "fused: of the fully fused lower bound (read x, write y, weights once) -- above 100% means fewer",
-           "HBM bytes than the kernel pipeline would move",
+           "roofline: the dominant kernel's algorithmic bytes or FLOPs per launch / its HIP-event time,",
+           "as a fraction of HBM or FP16 MFMA peak; fused: the whole forward against its lower bound",
+           "max(FLOPs / MFMA peak, (x + y + weights) / HBM peak)",
            f"{'shape':>5}  {'status':6}  {'tokens/s':>11}  {'ms':>10}  {'bound':5}  {'roofline':>8}  "
            f"{'fused':>11}  accuracy"]
     for r in results:

@@ -25,7 +25,7 @@ LIBRARY_PATH = Path(
 )
 
 # Constants mirrored from include/xblock.h.
-XB_ABI_VERSION = 2
+XB_ABI_VERSION = 3
 XB_F32 = 0
 XB_F16 = 1
 XB_EPI_BIAS = 0
@@ -38,6 +38,13 @@ XB_MASK_OUTPUT = 4
 XB_SPLIT_SPINS_DEFAULT = -1
 XB_SPLIT_FAULT_NO_PUBLISH = 1
 XB_DECODE_SCRATCH_BYTES = 32 << 20
+XB_VARIANT_AUTO = -1
+XB_OP_LINEAR = 0
+XB_OP_ATTENTION = 1
+XB_OP_FUSED_D128 = 2
+XB_FUSED_PAIRS = 0
+XB_FUSED_SPLIT = 1
+XB_FUSED_HD128 = 2
 
 EXPORTED_SYMBOLS = (
     "xb_abi_version",
@@ -46,8 +53,14 @@ EXPORTED_SYMBOLS = (
     "xb_residual_layernorm",
     "xb_residual_layernorm_masked",
     "xb_linear",
+    "xb_linear_v",
     "xb_attention_causal",
     "xb_attention",
+    "xb_attention_v",
+    "xb_select_linear",
+    "xb_select_attention",
+    "xb_select_fused_d128",
+    "xb_variant_name",
     "xb_kv_cache_append",
     "xb_attention_kv_cache_workspace_bytes",
     "xb_attention_kv_cache",
@@ -78,6 +91,12 @@ _SIGNATURES = {
     "xb_linear": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, ctypes.c_int, _vp]),
     "xb_attention_causal": (ctypes.c_int, [_vp, _vp, _i32, _i64, _i32, _i32, _f32, _vp]),
     "xb_attention": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i64, _i32, _i32, _f32, _i32, _vp]),
+    "xb_linear_v": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, ctypes.c_int, ctypes.c_int, _vp]),
+    "xb_attention_v": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i64, _i32, _i32, _f32, _i32, ctypes.c_int, _vp]),
+    "xb_select_linear": (ctypes.c_int, [_i64, _i32, _i32, ctypes.c_int]),
+    "xb_select_attention": (ctypes.c_int, [_i32, _i64, _i32, _i32, _i32]),
+    "xb_select_fused_d128": (ctypes.c_int, [_i64, _i32, _i32, _i32, _i32, _i32]),
+    "xb_variant_name": (ctypes.c_char_p, [ctypes.c_int, ctypes.c_int]),
     "xb_kv_cache_append": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i64, _i32, _i32, _i64, _i64, _vp]),
     "xb_attention_kv_cache_workspace_bytes": (_i64, [_i32, _i64, _i32, _i32, _i64]),
     "xb_attention_kv_cache": (

@@ -1,14 +1,27 @@
-"""Exact batch slicing with one hipGraph per chunk shape.
+"""Exact batch slicing, optionally with one hipGraph per chunk shape.
 
-Same contract as the reference's batch_chunk_runner.py:11-154: batch elements
-are independent (README.md:260-263), so running slices is exact; with
-`all_tokens_valid` the all-True mask is dropped and one graph serves every
-full chunk plus one for the remainder.  Each chunk graph has static input and
-output buffers (copy in, replay, copy out).
+Public name and constructor are the reference's `BatchChunkedTransformer`
+(batch_chunk_runner.py:49-154, used for official shape 6 at chunk 1024,
+torch_transformer_benchmark.py:1740, :1826-1846).  Batch elements are
+independent (README.md:260-263), so the output equals the whole-batch
+forward bit for bit.
 
-On one MI355X the whole official batch fits in HBM, so the point of chunking
-here is not capacity but locality: a chunk's activations can stay resident in
-the 256 MB Infinity Cache between the kernels of one forward.
+Design:
+  * Graphs (use_cuda_graphs, only for inputs whose mask is all True, as the
+    caller asserts with all_tokens_valid) are keyed by the chunk's batch size:
+    one for the full chunk, one for the remainder.  Each `_ChunkShapeGraph`
+    owns a static input buffer of its shape and a `graph_runner.CapturedCall`
+    of the model over it; a chunk is copied into the static input (device to
+    device), the graph replayed, and the static output copied into the
+    caller's output slice.  The copies are part of the contract: the captured
+    kernels have their buffer addresses baked in, and callers pass a new
+    input tensor on every call.
+  * Without graphs each chunk is one eager forward written straight into the
+    output slice (no copies).
+  * `chunk_size_for_memory` sizes a chunk from a byte budget (default: a
+    fraction of the GPU's free memory) with the model's own working-set
+    estimate; one MI355X (288 GB) holds every official batch whole, so the
+    model's execution plan only chunks batches beyond that.
 """
 
 from __future__ import annotations
@@ -18,37 +31,37 @@ from typing import Dict, Optional
 import torch
 import torch.nn as nn
 
+from .graph_runner import CapturedCall
 
-class _ChunkGraph:
-    def __init__(self, model: nn.Module, example: torch.Tensor, warmup_iterations: int = 3) -> None:
-        if not example.is_cuda:
-            raise ValueError("chunk graphs require GPU inputs")
-        if model.training:
-            raise ValueError("chunk graphs require model.eval()")
-        self.static_input = torch.empty_like(example)
-        self.static_input.copy_(example)
-        device = example.device
-        current = torch.cuda.current_stream(device)
-        side = torch.cuda.Stream(device=device)
-        side.wait_stream(current)
-        with torch.inference_mode(), torch.cuda.stream(side):
-            for _ in range(warmup_iterations):
-                model(self.static_input, None)
-        current.wait_stream(side)
-        torch.cuda.synchronize(device)
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.inference_mode(), torch.cuda.graph(self.graph):
-            self.static_output = model(self.static_input, None)
-        torch.cuda.synchronize(device)
 
-    def run_into(self, inputs: torch.Tensor, destination: torch.Tensor) -> None:
-        self.static_input.copy_(inputs)
-        self.graph.replay()
-        destination.copy_(self.static_output)
+class _ChunkShapeGraph:
+    """A captured forward over a static [chunk, S, D] input buffer."""
+
+    def __init__(self, model: nn.Module, like: torch.Tensor) -> None:
+        self.static_input = like.detach().clone()
+        with torch.inference_mode():
+            self.call = CapturedCall(lambda: model(self.static_input, None), like.device)
+
+    def run_into(self, chunk: torch.Tensor, destination: torch.Tensor) -> None:
+        self.static_input.copy_(chunk)
+        destination.copy_(self.call.replay())
+
+
+def chunk_size_for_memory(model: nn.Module, x: torch.Tensor, budget_bytes: Optional[int] = None) -> int:
+    """Largest batch slice whose forward working set fits `budget_bytes`.
+
+    The default budget is 80% of the device's free memory.  Returns the
+    whole batch when it fits, and at least 1.
+    """
+    per_sequence = model.activation_bytes(1, x.shape[1])
+    if budget_bytes is None:
+        free, _total = torch.cuda.mem_get_info(x.device)
+        budget_bytes = int(0.8 * free)
+    return max(1, min(x.shape[0], int(budget_bytes // max(1, per_sequence))))
 
 
 class BatchChunkedTransformer(nn.Module):
-    """Execute independent batch slices (BCR:49-154)."""
+    """Runs `model` over batch slices of `chunk_size` (BCR:49-154)."""
 
     def __init__(self, model: nn.Module, chunk_size: int, *, all_tokens_valid: bool, use_cuda_graphs: bool) -> None:
         super().__init__()
@@ -57,49 +70,49 @@ class BatchChunkedTransformer(nn.Module):
         if model.training:
             raise ValueError("batch chunking requires model.eval()")
         self.model = model
-        self.chunk_size = chunk_size
-        self.all_tokens_valid = all_tokens_valid
-        self.use_cuda_graphs = use_cuda_graphs and all_tokens_valid and torch.cuda.is_available()
+        self.chunk_size = int(chunk_size)
+        self.all_tokens_valid = bool(all_tokens_valid)
+        # Graph replays assume the mask the capture saw; only an all-valid batch qualifies.
+        self.use_cuda_graphs = bool(use_cuda_graphs) and self.all_tokens_valid and torch.cuda.is_available()
         self._uses_internal_cuda_graphs = self.use_cuda_graphs
-        self._chunk_graphs: Dict[tuple, Optional[_ChunkGraph]] = {}
-        self._chunk_graph_failures: Dict[tuple, str] = {}
-        self.training = False
+        self._graphs: Dict[tuple, _ChunkShapeGraph] = {}
+        self._graph_errors: Dict[tuple, str] = {}
+        self.eval()
 
     @property
     def graph_status(self) -> str:
         if not self.use_cuda_graphs:
             return "disabled"
-        if self._chunk_graph_failures:
-            return "partial fallback: " + "; ".join(sorted(set(self._chunk_graph_failures.values())))
-        return "reusable per-chunk hipGraph replay"
+        if self._graph_errors:
+            failed = ", ".join(f"chunk {key[0]}: {err}" for key, err in sorted(self._graph_errors.items()))
+            return f"eager for chunk shapes whose capture failed ({failed})"
+        return f"one hipGraph per chunk shape ({len(self._graphs)} captured)"
 
-    @staticmethod
-    def _graph_key(chunk: torch.Tensor) -> tuple:
-        return (tuple(chunk.shape), chunk.dtype, chunk.device.type, chunk.device.index)
-
-    def _run_chunk(self, inputs: torch.Tensor, valid_mask: Optional[torch.Tensor], destination: torch.Tensor) -> None:
-        if not self.use_cuda_graphs:
-            destination.copy_(self.model(inputs, valid_mask))
-            return
-        key = self._graph_key(inputs)
-        if key not in self._chunk_graphs:
-            try:
-                self._chunk_graphs[key] = _ChunkGraph(self.model, inputs)
-            except (RuntimeError, ValueError) as error:
-                self._chunk_graphs[key] = None
-                self._chunk_graph_failures[key] = str(error)
-        graph = self._chunk_graphs[key]
+    def _graph_for(self, chunk: torch.Tensor) -> Optional[_ChunkShapeGraph]:
+        key = (chunk.shape[0], tuple(chunk.shape[1:]), chunk.dtype, chunk.device)
+        if key in self._graph_errors:
+            return None
+        graph = self._graphs.get(key)
         if graph is None:
-            destination.copy_(self.model(inputs, None))
-        else:
-            graph.run_into(inputs, destination)
+            try:
+                graph = _ChunkShapeGraph(self.model, chunk)
+            except (RuntimeError, ValueError) as error:
+                self._graph_errors[key] = str(error)
+                return None
+            self._graphs[key] = graph
+        return graph
 
     def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
         if x.ndim != 3:
-            raise ValueError("batch-chunked Transformer input must be 3-D")
-        chunk_mask = None if (self.all_tokens_valid or valid_token_mask is None) else valid_token_mask
+            raise ValueError("batch-chunked Transformer input must be [B, S, D]")
+        mask = None if self.all_tokens_valid else valid_token_mask
         output = torch.empty_like(x)
         for start in range(0, x.shape[0], self.chunk_size):
             end = min(start + self.chunk_size, x.shape[0])
-            self._run_chunk(x[start:end], None if chunk_mask is None else chunk_mask[start:end], output[start:end])
+            chunk = x[start:end]
+            graph = self._graph_for(chunk) if self.use_cuda_graphs else None
+            if graph is not None:
+                graph.run_into(chunk, output[start:end])
+            else:
+                output[start:end].copy_(self.model(chunk, None if mask is None else mask[start:end]))
         return output

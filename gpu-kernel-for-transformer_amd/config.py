@@ -78,20 +78,65 @@ _OFFICIAL_SHAPE_IDS_BY_CONFIG = {
 }
 
 
+# One MI355X: 288 GB of HBM3E.  A batch whose forward working set exceeds
+# this share of it runs in independent slices (batch elements are
+# independent, README.md:260-263); every official batch fits whole.
+HBM_BYTES = 288e9
+CHUNK_BUDGET_FRACTION = 0.6
+
+
+def forward_working_set_bytes(config: TransformerConfig, batch: int, seq_len: int, fused: bool = False) -> int:
+    """Device bytes one forward of [batch, seq_len] keeps alive, input and output included.
+
+    Per-op path: x and y (FP32), the FP32 residual stream, and the FP16
+    intermediates (LayerNorm outputs, packed QKV, attention context, the two
+    projection updates, FFN hidden), counted as if all were live at once.
+    The whole-stack kernel keeps only x and y.
+    """
+    d, f = config.d_model, config.ffn_dim
+    per_token = 8 * d if fused else 4 * d + 4 * d + 4 * d + 2 * (d + 3 * d + d + d + d + f + d)
+    return int(batch) * int(seq_len) * per_token
+
+
 @dataclass(frozen=True)
 class ShapeExecutionPlan:
-    """Kernel choices for one exact official shape (torch_transformer_benchmark.py:98-123).
+    """The kernels one forward runs on gfx950 (torch_transformer_benchmark.py:98-157).
 
-    ffn_strategy / attention_strategy / projection_strategy name the gfx950
-    kernels the forward pass uses; batch_chunk_size > 0 runs the batch in
-    independent slices (torch_transformer_benchmark.py:1022-1049).
+    Built by `resolve_shape_execution_plan` from the library's own selection
+    functions (xb_select_*), and read back by the model's forward, so
+    `describe()` names what actually runs.  ffn / attention / projection
+    strategies keep the reference's field names; `forward_strategy` is the
+    whole-stack kernel form (`fused_stack_*`) or `per_op`, and the *_variant
+    fields are the ids the model passes to the kernels (-1: not used).
+    batch_chunk_size > 0 runs the batch in independent slices
+    (torch_transformer_benchmark.py:1022-1049).
     """
 
     official_shape_id: Optional[int]
-    ffn_strategy: str = "mfma_gemm_gelu"
-    attention_strategy: str = "flash_causal"
-    projection_strategy: str = "mfma_gemm"
+    ffn_strategy: str = "unresolved"
+    attention_strategy: str = "unresolved"
+    projection_strategy: str = "unresolved"
     batch_chunk_size: int = 0
+    forward_strategy: str = "unresolved"
+    arch: str = "gfx950"
+    batch: int = 0
+    seq_len: int = 0
+    masked: bool = False
+    fused_variant: int = -1
+    qkv_variant: int = -1
+    out_variant: int = -1
+    ffn_in_variant: int = -1
+    ffn_out_variant: int = -1
+    attention_variant: int = -1
+
+    @property
+    def fused(self) -> bool:
+        return self.fused_variant >= 0
+
+    @property
+    def runnable(self) -> bool:
+        """Whether every step has a gfx950 kernel (else forward_strategy says why not)."""
+        return self.fused or self.attention_variant >= 0
 
     def describe(self) -> str:
         shape = (
@@ -107,18 +152,74 @@ class ShapeExecutionPlan:
         return (
             f"{shape}: ffn={self.ffn_strategy}, "
             f"attention={self.attention_strategy}, "
-            f"projections={self.projection_strategy}{chunk}"
+            f"projections={self.projection_strategy}{chunk}; "
+            f"forward={self.forward_strategy} on {self.arch} "
+            f"(B={self.batch}, S={self.seq_len}{', padded' if self.masked else ''})"
         )
 
 
-def resolve_shape_execution_plan(config: TransformerConfig) -> ShapeExecutionPlan:
-    """Per-shape plan (torch_transformer_benchmark.py:131-157).
+def _variant_name(lib, op: int, variant: int) -> str:
+    name = lib.xb_variant_name(op, variant)
+    return name.decode() if name else f"variant-{variant}"
 
-    Every shape runs the same kernel families on gfx950; batch elements are
-    independent (README.md:260-263), so only the chunk size is shape tuned.
-    One MI355X holds the whole of every official batch in HBM, so chunking is
-    off by default; `_large_batch_chunk_size` can still be set by the caller
-    exactly as the reference's main() does (torch_transformer_benchmark.py:1740).
+
+def resolve_shape_execution_plan(
+    config: TransformerConfig,
+    batch: Optional[int] = None,
+    seq_len: Optional[int] = None,
+    masked: bool = False,
+    fused_allowed: bool = True,
+) -> ShapeExecutionPlan:
+    """The gfx950 plan for a forward of [batch, seq_len] (default: the config's own shape).
+
+    masked: a padding mask with at least one False (the key-masked kernel
+    forms).  fused_allowed: the caller's whole-stack
+    conditions beyond the shape (the toggle, LayerNorm eps 1e-5 with affine
+    parameters).  The kernel choices are the library's (xb_select_*); only a
+    batch whose working set exceeds CHUNK_BUDGET_FRACTION of HBM is chunked.
+    Without the library the plan stays "unresolved" (the forward then raises).
     """
-    shape_id = _OFFICIAL_SHAPE_IDS_BY_CONFIG.get(config)
-    return ShapeExecutionPlan(official_shape_id=shape_id, batch_chunk_size=0)
+    from . import _capi
+
+    b = config.batch_size if batch is None else int(batch)
+    s = config.seq_len if seq_len is None else int(seq_len)
+    shape_id = _OFFICIAL_SHAPE_IDS_BY_CONFIG.get(config) if (b, s) == (config.batch_size, config.seq_len) else None
+    masked = bool(masked)
+    if not _capi.XBLOCK_AVAILABLE:
+        return ShapeExecutionPlan(official_shape_id=shape_id, batch=b, seq_len=s, masked=masked,
+                                  forward_strategy=f"unresolved ({_capi.XBLOCK_LOAD_ERROR})")
+    lib = _capi.lib()
+    d, f, h = config.d_model, config.ffn_dim, config.num_heads
+    fused = lib.xb_select_fused_d128(b, s, h, f, int(config.causal), int(masked)) if (fused_allowed and d == 128) else -1
+    budget = CHUNK_BUDGET_FRACTION * HBM_BYTES
+    per_seq = forward_working_set_bytes(config, 1, s, fused=fused >= 0)
+    chunk = 0 if per_seq * b <= budget else max(1, int(budget // per_seq))
+    if fused >= 0:
+        name = _variant_name(lib, _capi.XB_OP_FUSED_D128, fused)
+        return ShapeExecutionPlan(
+            official_shape_id=shape_id, batch=b, seq_len=s, masked=masked, batch_chunk_size=chunk,
+            forward_strategy=f"{name} (one launch for all layers)", fused_variant=fused,
+            ffn_strategy=f"{name}: MFMA GEMMs + erf GELU in registers",
+            attention_strategy=f"{name}: {'causal' if config.causal else 'full'} attention, K/V^T in LDS",
+            projection_strategy=f"{name}: MFMA GEMMs, weights staged in LDS",
+        )
+    rows = (chunk or b) * s
+    qkv = lib.xb_select_linear(rows, 3 * d, d, _capi.XB_EPI_BIAS)
+    out = lib.xb_select_linear(rows, d, d, _capi.XB_EPI_BIAS)
+    ffn_in = lib.xb_select_linear(rows, f, d, _capi.XB_EPI_BIAS_GELU)
+    ffn_out = lib.xb_select_linear(rows, d, f, _capi.XB_EPI_BIAS)
+    attn = lib.xb_select_attention(chunk or b, s, h, d // h, int(masked))
+    missing = [f"{what}: {lib.xb_strerror(code).decode()}" for what, code in
+               (("qkv", qkv), ("out", out), ("ffn_in", ffn_in), ("ffn_out", ffn_out), ("attention", attn)) if code < 0]
+    if missing:
+        return ShapeExecutionPlan(official_shape_id=shape_id, batch=b, seq_len=s, masked=masked, batch_chunk_size=chunk,
+                                  forward_strategy="unsupported (" + "; ".join(missing) + ")")
+    lin = lambda v: _variant_name(lib, _capi.XB_OP_LINEAR, v)  # noqa: E731
+    return ShapeExecutionPlan(
+        official_shape_id=shape_id, batch=b, seq_len=s, masked=masked, batch_chunk_size=chunk,
+        forward_strategy="per_op (LayerNorm, QKV GEMM, attention, out GEMM, residual LayerNorm, FFN GEMMs per layer)",
+        ffn_strategy=f"{lin(ffn_in)}+gelu_erf / {lin(ffn_out)}",
+        attention_strategy=_variant_name(lib, _capi.XB_OP_ATTENTION, attn),
+        projection_strategy=f"qkv {lin(qkv)}, out {lin(out)}",
+        qkv_variant=qkv, out_variant=out, ffn_in_variant=ffn_in, ffn_out_variant=ffn_out, attention_variant=attn,
+    )

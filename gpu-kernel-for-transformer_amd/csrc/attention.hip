@@ -803,31 +803,53 @@ static hipError_t launch_attn_pp(AttnArgs a, int B, int causal, hipStream_t s) {
   return hipGetLastError();
 }
 
-// Query ranges of at least kPingPongMinQueries (head_dim 64, no key mask) take
-// the ping-pong kernel (512 queries per block); other long ranges take 64
-// queries per wave (each K/V fragment read from LDS then feeds 4 MFMAs);
-// short ones keep 32 so a block does not outgrow S_q.
-constexpr int kPingPongMinQueries = 4096;
+constexpr int kPingPongMinQueries = 4096;  // query ranges from here on take the ping-pong kernel
 constexpr int kCUs = 256;  // MI355X compute units
 
+// Kernel variants (XB_ATTN_*) and the head widths each is built for.
+static bool attention_variant_fits(int variant, int hd, bool masked) {
+  switch (variant) {
+    case XB_ATTN_W4_Q16: case XB_ATTN_W8_Q16: return hd == 256;
+    case XB_ATTN_W4_Q32: return hd <= 128;
+    case XB_ATTN_W4_Q64: return hd <= 64;
+    case XB_ATTN_PINGPONG: return hd == 64 && !masked;
+    default: return false;
+  }
+}
+
+// The library's choice.  head_dim 256 up to 128 queries: one 8-wave block
+// takes all of them, so each K/V row is fetched once per (batch, head)
+// instead of by two 64-query blocks (cfg3's geometry: 16.7 vs 18.6 us) -- when
+// the B*H blocks still fill the GPU.  head_dim 64 without a key mask from
+// kPingPongMinQueries on: the ping-pong kernel.  Other long ranges take 64
+// queries per wave (each K/V fragment read from LDS then feeds 4 MFMAs);
+// short ones keep 32 so a block does not outgrow S_q.
+static int select_attention(int64_t B, int S_q, int H, int hd, bool masked) {
+  if (hd >= 256) return S_q <= 128 && B * H >= kCUs ? XB_ATTN_W8_Q16 : XB_ATTN_W4_Q16;
+  if (hd >= 128) return XB_ATTN_W4_Q32;
+  if (hd == 64 && !masked && S_q >= kPingPongMinQueries) return XB_ATTN_PINGPONG;
+  return S_q >= 1024 ? XB_ATTN_W4_Q64 : XB_ATTN_W4_Q32;
+}
+
 template <int HD>
-static hipError_t dispatch_attn(const AttnArgs& a, int B, int causal, hipStream_t s) {
+static hipError_t run_attn(int variant, const AttnArgs& a, int B, int causal, hipStream_t s) {
   if constexpr (HD >= 256) {
-    // Up to 128 queries: one 8-wave block takes all of them, so each K/V row
-    // is fetched once per (batch, head) instead of by two 64-query blocks
-    // (cfg3's geometry: 16.7 vs 18.6 us) -- when the B*H blocks still fill
-    // the GPU.
-    if (a.S_q <= 128 && (int64_t)B * a.H >= kCUs) return launch_attn<HD, 1, 8>(a, B, causal, s);
+    if (variant == XB_ATTN_W8_Q16) return launch_attn<HD, 1, 8>(a, B, causal, s);
     return launch_attn<HD, 1>(a, B, causal, s);
   } else if constexpr (HD >= 128) {
     return launch_attn<HD, 2>(a, B, causal, s);
   } else {
     if constexpr (HD == 64) {
-      if (a.key_valid == nullptr && a.S_q >= kPingPongMinQueries) return launch_attn_pp<HD>(a, B, causal, s);
+      if (variant == XB_ATTN_PINGPONG) return launch_attn_pp<HD>(a, B, causal, s);
     }
-    if (a.S_q >= 1024) return launch_attn<HD, 4>(a, B, causal, s);
+    if (variant == XB_ATTN_W4_Q64) return launch_attn<HD, 4>(a, B, causal, s);
     return launch_attn<HD, 2>(a, B, causal, s);
   }
+}
+
+template <int HD>
+static hipError_t dispatch_attn(const AttnArgs& a, int B, int causal, hipStream_t s) {
+  return run_attn<HD>(select_attention(B, a.S_q, a.H, HD, a.key_valid != nullptr), a, B, causal, s);
 }
 
 // Decode (at most kDecodeQueries new tokens per sequence): one-wave blocks,
@@ -915,12 +937,28 @@ static hipError_t by_head_dim(int hd, F&& f) {
 
 using namespace xb;
 
-extern "C" int xb_attention(const void* qkv, void* out, const uint8_t* key_valid, int32_t batch,
-                            int64_t seq_len, int32_t heads, int32_t head_dim, float scale, int32_t causal,
-                            void* stream) {
+static int check_attention(int32_t batch, int64_t seq_len, int32_t heads, int32_t head_dim) {
   if (batch < 0 || seq_len < 0 || heads <= 0 || head_dim <= 0) return XB_ERR_BAD_SIZE;
   if (seq_len > 0x7fffffffLL / 4) return XB_ERR_BAD_SIZE;
+  if (3LL * heads * head_dim > 0x7fffffffLL) return XB_ERR_BAD_SIZE;
   if (!supported_head_dim(head_dim)) return XB_ERR_UNSUPPORTED_SHAPE;
+  return XB_OK;
+}
+
+extern "C" int xb_select_attention(int32_t batch, int64_t seq_len, int32_t heads, int32_t head_dim,
+                                   int32_t masked) {
+  const int bad = check_attention(batch, seq_len, heads, head_dim);
+  return bad ? bad : select_attention(batch, (int)seq_len, heads, head_dim, masked != 0);
+}
+
+extern "C" int xb_attention_v(const void* qkv, void* out, const uint8_t* key_valid, int32_t batch,
+                              int64_t seq_len, int32_t heads, int32_t head_dim, float scale, int32_t causal,
+                              int variant, void* stream) {
+  const int bad = check_attention(batch, seq_len, heads, head_dim);
+  if (bad) return bad;
+  const bool masked = key_valid != nullptr;
+  if (variant == XB_VARIANT_AUTO) variant = select_attention(batch, (int)seq_len, heads, head_dim, masked);
+  if (!attention_variant_fits(variant, head_dim, masked)) return XB_ERR_BAD_VARIANT;
   if (batch == 0 || seq_len == 0) return XB_OK;  // empty tensors may carry NULL data pointers
   if (!qkv || !out) return XB_ERR_NULL_POINTER;
   if (((uintptr_t)qkv | (uintptr_t)out) & 15u) return XB_ERR_MISALIGNED;
@@ -940,10 +978,16 @@ extern "C" int xb_attention(const void* qkv, void* out, const uint8_t* key_valid
   a.H = heads;
   a.S_q = a.S_k = S;
   a.scale_log2 = scale * 1.44269504088896340736f;
-  if (3 * D > 0x7fffffffLL) return XB_ERR_BAD_SIZE;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int c = causal ? 1 : 0;
-  return (int)by_head_dim(head_dim, [&](auto hd) { return dispatch_attn<decltype(hd)::value>(a, batch, c, s); });
+  return (int)by_head_dim(head_dim, [&](auto hd) { return run_attn<decltype(hd)::value>(variant, a, batch, c, s); });
+}
+
+extern "C" int xb_attention(const void* qkv, void* out, const uint8_t* key_valid, int32_t batch,
+                            int64_t seq_len, int32_t heads, int32_t head_dim, float scale, int32_t causal,
+                            void* stream) {
+  return xb_attention_v(qkv, out, key_valid, batch, seq_len, heads, head_dim, scale, causal, XB_VARIANT_AUTO,
+                        stream);
 }
 
 extern "C" int xb_attention_causal(const void* qkv, void* out, int32_t batch, int64_t seq_len,

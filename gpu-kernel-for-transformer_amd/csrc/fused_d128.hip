@@ -1265,6 +1265,16 @@ extern "C" int xb_fused_forward_d128(const float* x, float* y, const void* wpack
                        nullptr, 0, -1, 0, stream);
 }
 
+extern "C" int xb_select_fused_d128(int64_t batch, int32_t seq_len, int32_t heads, int32_t ffn_dim, int32_t causal,
+                                    int32_t masked) {
+  if (batch < 0 || seq_len <= 0 || heads <= 0 || ffn_dim <= 0) return XB_ERR_BAD_SIZE;
+  if (seq_len > fused::SMAX || fused::D % heads != 0 || ffn_dim != 128) return XB_ERR_UNSUPPORTED_SHAPE;
+  const int hd = fused::D / heads;
+  if (hd != 8 && hd != 16 && hd != 32 && hd != 64 && hd != 128) return XB_ERR_UNSUPPORTED_SHAPE;
+  if (hd == 128) return (masked || !causal) ? XB_ERR_UNSUPPORTED_SHAPE : XB_FUSED_HD128;
+  return fused::use_split(batch, seq_len, hd, causal) ? XB_FUSED_SPLIT : XB_FUSED_PAIRS;
+}
+
 extern "C" int64_t xb_fused_forward_d128_workspace_bytes(int64_t batch, int32_t seq_len, int32_t heads,
                                                          int32_t layers, int32_t causal) {
   if (batch <= 0 || seq_len <= 0 || heads <= 0 || layers <= 0 || fused::D % heads != 0) return 0;

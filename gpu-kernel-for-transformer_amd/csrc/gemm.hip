@@ -319,37 +319,75 @@ static hipError_t launch_gemm(const half_t* a, const half_t* w, const float* bia
   return hipGetLastError();
 }
 
-template <int EPI>
-static hipError_t dispatch_gemm(const half_t* a, const half_t* w, const float* bias, half_t* c,
-                                int64_t m, int n, int k, hipStream_t s) {
+// Tile variants (XB_LINEAR_*): the gemm_dma_kernel tiles need K % 64 == 0
+// and K >= 256 (256 x 192 also N % 192 == 0); the gemm_nt_kernel tiles take
+// any K % 8 == 0.
+static bool linear_variant_fits(int variant, int64_t m, int n, int k) {
+  (void)m;
+  const bool dma = k % 64 == 0 && k >= 256;
+  switch (variant) {
+    case XB_LINEAR_DMA_256x256: case XB_LINEAR_DMA_128x256: case XB_LINEAR_DMA_128x128: return dma;
+    case XB_LINEAR_DMA_256x192: return dma && n % 192 == 0;
+    case XB_LINEAR_NT_128x128: case XB_LINEAR_NT_64x64: return true;
+    default: return false;
+  }
+}
+
+// The library's choice for a shape.  With the DMA tiles one block runs per
+// CU, so the cost is taken as rounds of 256 tiles x tile area, the 256 x 256
+// tile ~15% cheaper per output (fewer LDS bytes per MFMA); 256 x 192 sits
+// between them and fills whole rounds where 256 x 256 leaves half a round
+// idle (M = 8192, N = 3072: 63 vs 70 us).
+static int select_linear(int64_t m, int n, int k) {
   auto tiles = [&](int64_t bm, int64_t bn) { return ((m + bm - 1) / bm) * ((n + bn - 1) / bn); };
   if (k % 64 == 0 && k >= 256) {
-    // One block per CU: cost ~ rounds of 256 tiles x tile area, with the
-    // 256 x 256 tile ~15% cheaper per output (fewer LDS bytes per MFMA).
-    // 256 x 192 (N % 192 == 0) sits between them: it fills whole rounds where
-    // 256 x 256 leaves half a round idle (M = 8192, N = 3072: 63 vs 70 us).
     const int64_t big = (tiles(256, 256) + 255) / 256 * 65536 * 85 / 100;
     const int64_t wide = n % 192 == 0 ? (tiles(256, 192) + 255) / 256 * 49152 * 90 / 100 : INT64_MAX;
     const int64_t mid = (tiles(128, 256) + 255) / 256 * 32768;
     const int64_t small = (tiles(128, 128) + 255) / 256 * 16384 * 115 / 100;
-    if (big <= wide && big <= mid && big <= small) return launch_gemm_dma<256, 256, 4, 2, EPI, 2>(a, w, bias, c, m, n, k, s);
-    if (wide <= mid && wide <= small) return launch_gemm_dma<256, 192, 4, 2, EPI, 2>(a, w, bias, c, m, n, k, s);
-    if (mid <= small) return launch_gemm_dma<128, 256, 2, 4, EPI, 2>(a, w, bias, c, m, n, k, s);
-    return launch_gemm_dma<128, 128, 2, 2, EPI, 2>(a, w, bias, c, m, n, k, s);
+    if (big <= wide && big <= mid && big <= small) return XB_LINEAR_DMA_256x256;
+    if (wide <= mid && wide <= small) return XB_LINEAR_DMA_256x192;
+    if (mid <= small) return XB_LINEAR_DMA_128x256;
+    return XB_LINEAR_DMA_128x128;
   }
-  if (tiles(128, 128) >= 512) return launch_gemm<128, 128, 2, 2, EPI>(a, w, bias, c, m, n, k, s);
-  return launch_gemm<64, 64, 2, 2, EPI>(a, w, bias, c, m, n, k, s);
+  return tiles(128, 128) >= 512 ? XB_LINEAR_NT_128x128 : XB_LINEAR_NT_64x64;
+}
+
+template <int EPI>
+static hipError_t run_gemm(int variant, const half_t* a, const half_t* w, const float* bias, half_t* c,
+                           int64_t m, int n, int k, hipStream_t s) {
+  switch (variant) {
+    case XB_LINEAR_DMA_256x256: return launch_gemm_dma<256, 256, 4, 2, EPI, 2>(a, w, bias, c, m, n, k, s);
+    case XB_LINEAR_DMA_256x192: return launch_gemm_dma<256, 192, 4, 2, EPI, 2>(a, w, bias, c, m, n, k, s);
+    case XB_LINEAR_DMA_128x256: return launch_gemm_dma<128, 256, 2, 4, EPI, 2>(a, w, bias, c, m, n, k, s);
+    case XB_LINEAR_DMA_128x128: return launch_gemm_dma<128, 128, 2, 2, EPI, 2>(a, w, bias, c, m, n, k, s);
+    case XB_LINEAR_NT_128x128: return launch_gemm<128, 128, 2, 2, EPI>(a, w, bias, c, m, n, k, s);
+    default: return launch_gemm<64, 64, 2, 2, EPI>(a, w, bias, c, m, n, k, s);
+  }
 }
 
 }  // namespace xb
 
 using namespace xb;
 
-extern "C" int xb_linear(const void* a, const void* w, const float* bias, void* c,
-                         int64_t m, int32_t n, int32_t k, int epilogue, void* stream) {
+static int check_linear(int64_t m, int32_t n, int32_t k, int epilogue) {
   if (m < 0 || n <= 0 || k <= 0 || m > 0x7fffffffLL) return XB_ERR_BAD_SIZE;
   if (n % 8 != 0 || k % 8 != 0) return XB_ERR_UNSUPPORTED_SHAPE;
   if (epilogue != XB_EPI_BIAS && epilogue != XB_EPI_BIAS_GELU) return XB_ERR_BAD_EPILOGUE;
+  return XB_OK;
+}
+
+extern "C" int xb_select_linear(int64_t m, int32_t n, int32_t k, int epilogue) {
+  const int bad = check_linear(m, n, k, epilogue);
+  return bad ? bad : select_linear(m, n, k);
+}
+
+extern "C" int xb_linear_v(const void* a, const void* w, const float* bias, void* c, int64_t m, int32_t n,
+                           int32_t k, int epilogue, int variant, void* stream) {
+  const int bad = check_linear(m, n, k, epilogue);
+  if (bad) return bad;
+  if (variant == XB_VARIANT_AUTO) variant = select_linear(m, n, k);
+  if (!linear_variant_fits(variant, m, n, k)) return XB_ERR_BAD_VARIANT;
   if (m == 0) return XB_OK;  // empty tensors may carry NULL data pointers
   if (!a || !w || !c) return XB_ERR_NULL_POINTER;
   if (((uintptr_t)a | (uintptr_t)w | (uintptr_t)c) & 15u) return XB_ERR_MISALIGNED;
@@ -358,7 +396,12 @@ extern "C" int xb_linear(const void* a, const void* w, const float* bias, void* 
   const half_t* Wt = static_cast<const half_t*>(w);
   half_t* Cc = static_cast<half_t*>(c);
   hipError_t e = epilogue == XB_EPI_BIAS_GELU
-      ? dispatch_gemm<XB_EPI_BIAS_GELU>(A, Wt, bias, Cc, m, n, k, s)
-      : dispatch_gemm<XB_EPI_BIAS>(A, Wt, bias, Cc, m, n, k, s);
+      ? run_gemm<XB_EPI_BIAS_GELU>(variant, A, Wt, bias, Cc, m, n, k, s)
+      : run_gemm<XB_EPI_BIAS>(variant, A, Wt, bias, Cc, m, n, k, s);
   return (int)e;
+}
+
+extern "C" int xb_linear(const void* a, const void* w, const float* bias, void* c,
+                         int64_t m, int32_t n, int32_t k, int epilogue, void* stream) {
+  return xb_linear_v(a, w, bias, c, m, n, k, epilogue, XB_VARIANT_AUTO, stream);
 }

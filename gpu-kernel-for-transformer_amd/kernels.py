@@ -209,11 +209,13 @@ def linear(
     bias: Optional[torch.Tensor],
     gelu: bool = False,
     out: Optional[torch.Tensor] = None,
+    variant: int = _capi.XB_VARIANT_AUTO,
 ) -> torch.Tensor:
     """FP16 `inputs @ weight.T + bias` (optionally exact-erf GELU), FP32 accumulation.
 
     inputs: [..., K] float16 contiguous; weight: [N, K] float16 (nn.Linear
-    layout); bias: [N] float32 or None.  Returns [..., N] float16.
+    layout); bias: [N] float32 or None.  Returns [..., N] float16.  `variant`
+    is a tile variant (XB_LINEAR_*) from the execution plan, or auto.
     """
     _require_device(inputs, "linear")
     if weight.ndim != 2 or (bias is not None and bias.ndim != 1):
@@ -233,11 +235,11 @@ def linear(
         out = torch.empty((*inputs.shape[:-1], n), device=inputs.device, dtype=torch.float16)
     epi = XB_EPI_BIAS_GELU if gelu else XB_EPI_BIAS
     check(
-        _launch(f"gemm_n{n}_k{k}{'_gelu' if gelu else ''}", lambda: lib().xb_linear(
-            inputs.data_ptr(), weight.data_ptr(), _ptr(bias), out.data_ptr(), m, n, k, epi,
+        _launch(f"gemm_n{n}_k{k}{'_gelu' if gelu else ''}", lambda: lib().xb_linear_v(
+            inputs.data_ptr(), weight.data_ptr(), _ptr(bias), out.data_ptr(), m, n, k, epi, int(variant),
             stream_handle(inputs.device),
         )),
-        "xb_linear",
+        "xb_linear_v",
     )
     return out
 
@@ -274,6 +276,7 @@ def attention(
     causal: bool = True,
     scale: Optional[float] = None,
     out: Optional[torch.Tensor] = None,
+    variant: int = _capi.XB_VARIANT_AUTO,
 ) -> torch.Tensor:
     """Attention over a packed [B, S, 3*D] FP16 projection with optional key padding.
 
@@ -282,6 +285,7 @@ def attention(
     250-253); causal=False drops the causal mask.  A query that sees no key
     gets a zero row (the baseline's softmax would give NaN there, which its
     block then overwrites by zeroing the padded rows, TTB:263-264).
+    `variant` is a kernel variant (XB_ATTN_*) from the execution plan, or auto.
     """
     _require_device(qkv, "attention")
     if qkv.ndim != 3 or qkv.shape[-1] % (3 * num_heads) != 0:
@@ -298,11 +302,11 @@ def attention(
     valid = None if key_valid is None else _byte_mask(key_valid, batch * seq_len, qkv.device, "key_valid")
     name = f"attention_hd{head_dim}{'' if causal else '_full'}{'' if valid is None else '_masked'}"
     check(
-        _launch(name, lambda: lib().xb_attention(
+        _launch(name, lambda: lib().xb_attention_v(
             qkv.data_ptr(), out.data_ptr(), _ptr(valid), batch, seq_len, num_heads, head_dim,
-            float(scale), int(bool(causal)), stream_handle(qkv.device),
+            float(scale), int(bool(causal)), int(variant), stream_handle(qkv.device),
         )),
-        "xb_attention",
+        "xb_attention_v",
     )
     return out
 

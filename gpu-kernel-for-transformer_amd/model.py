@@ -45,7 +45,8 @@ import torch
 import torch.nn as nn
 
 from . import _capi, kernels
-from .config import ShapeExecutionPlan, TransformerConfig, resolve_shape_execution_plan
+from .config import (ShapeExecutionPlan, TransformerConfig, forward_working_set_bytes,
+                     resolve_shape_execution_plan)
 
 _LOG2E = 1.4426950408889634
 
@@ -142,7 +143,6 @@ class UserOptimizedTransformer(nn.Module):
             ]
         )
         self.final_norm = nn.LayerNorm(config.d_model)
-        self._shape_execution_plan = resolve_shape_execution_plan(config)
         # The gfx950 path computes GEMMs and attention in FP16 (FP32 accumulation,
         # FP32 residual stream); the reference reaches the same state through
         # enable_mixed_precision(torch.float16) (TTB:1750-1771).
@@ -150,8 +150,8 @@ class UserOptimizedTransformer(nn.Module):
         self._kv_cache_enabled = False
         self._kv_cache: Dict[int, Tuple[torch.Tensor, torch.Tensor]] = {}
         self._kv_cache_length = 0
-        self._large_batch_chunk_size = self._shape_execution_plan.batch_chunk_size
         self._fused_stack_enabled = True
+        self._large_batch_chunk_size = self.shape_execution_plan.batch_chunk_size
         self._strict_handoff_checks = False
         # Recorded for the reference's toggles (TTB:379-406); see their methods.
         self._triton_fused_norm_enabled = True
@@ -161,8 +161,30 @@ class UserOptimizedTransformer(nn.Module):
     # ----------------------------------------------------------------- toggles
     @property
     def shape_execution_plan(self) -> ShapeExecutionPlan:
-        """The immutable dispatch decision (TTB:364-367)."""
-        return self._shape_execution_plan
+        """The plan a forward of the config's own [batch_size, seq_len] input runs (TTB:364-367)."""
+        cfg = self.config
+        return self.execution_plan(cfg.batch_size, cfg.seq_len)
+
+    def execution_plan(self, batch: int, seq_len: int, padded: bool = False, per_op: bool = False) -> ShapeExecutionPlan:
+        """The kernels a forward of [batch, seq_len] runs (padded: a mask with a False), cached.
+
+        The forward reads its kernel choices from here, so `describe()` of
+        this plan names what runs.  Cached per shape and whole-stack
+        eligibility (the enable_fused_stack toggle, LayerNorm eps and affine);
+        per_op=True asks for the per-op sequence (KV-cached steps).
+        """
+        key = (int(batch), int(seq_len), bool(padded), self._fused_stack_eligible() and not per_op)
+        plans = self.__dict__.setdefault("_plans", {})
+        plan = plans.get(key)
+        if plan is None:
+            plan = resolve_shape_execution_plan(self.config, batch, seq_len, masked=padded, fused_allowed=key[3])
+            plans[key] = plan
+        return plan
+
+    def activation_bytes(self, batch: int, seq_len: int) -> int:
+        """Device bytes a forward of [batch, seq_len] keeps alive (input and output included)."""
+        plan = self.execution_plan(batch, seq_len)
+        return forward_working_set_bytes(self.config, batch, seq_len, fused=plan.fused)
 
     def enable_mixed_precision(self, dtype: Optional[torch.dtype] = torch.float16) -> None:
         """Select the compute dtype (TTB:369-377); the HIP path implements float16."""
@@ -258,18 +280,11 @@ class UserOptimizedTransformer(nn.Module):
             self.__dict__["_tree_cache"] = cached
         return cached[1], cached[2]
 
-    def _uses_fused_stack(self, x: torch.Tensor) -> bool:
-        """Shape contract of xb_fused_forward_d128."""
-        cfg = self.config
-        norms = self._tree()[1]
-        return (
-            self._fused_stack_enabled
-            and cfg.d_model == 128
-            and cfg.ffn_dim == 128
-            and x.shape[1] <= 128
-            and cfg.head_dim in kernels.FUSED_D128_HEAD_DIMS
-            and all(n.eps == 1e-5 and n.weight is not None and n.bias is not None for n in norms)
-        )
+    def _fused_stack_eligible(self) -> bool:
+        """Conditions of the whole-stack kernel beyond the shape: the toggle, LayerNorm eps 1e-5 with affine."""
+        if not self._fused_stack_enabled:
+            return False
+        return all(n.eps == 1e-5 and n.weight is not None and n.bias is not None for n in self._tree()[1])
 
     def _fused_stack_parameters(self) -> Tuple[torch.Tensor, torch.Tensor, int]:
         """Fragment-packed FP16 weights, FP32 bias/LayerNorm buffer and LayerNorm affine mask, cached by version."""
@@ -334,15 +349,15 @@ class UserOptimizedTransformer(nn.Module):
         Such a forward gains nothing from graph replay, which would only add
         the copy of the static output that every replay returns.
         """
-        chunk = self._large_batch_chunk_size
-        return (
-            valid_token_mask is None
-            and not self._kv_cache_enabled
-            and x.is_cuda and x.ndim == 3 and x.dtype == torch.float32 and x.is_contiguous()
-            and not (chunk and x.shape[0] > chunk)
-            and self._uses_fused_stack(x)
-            and (self.config.causal or self.config.head_dim <= 64)
-        )
+        if not (valid_token_mask is None and not self._kv_cache_enabled and x.is_cuda and x.ndim == 3
+                and x.dtype == torch.float32 and x.is_contiguous() and x.shape[-1] == self.config.d_model):
+            return False
+        chunk = self._chunk_size(x.shape[0], x.shape[1])
+        return self.execution_plan(x.shape[0], x.shape[1]).fused and not (chunk and x.shape[0] > chunk)
+
+    def _chunk_size(self, batch: int, seq_len: int) -> int:
+        """Batch slice per launch sequence: the caller's _large_batch_chunk_size (TTB:1740), else the plan's."""
+        return self._large_batch_chunk_size or self.execution_plan(batch, seq_len).batch_chunk_size
 
     def _all_tokens_valid(self, valid_token_mask: Optional[torch.Tensor], seq_len: int) -> bool:
         """Mask inspection cached by identity + version + length (TTB:464-522)."""
@@ -389,7 +404,7 @@ class UserOptimizedTransformer(nn.Module):
                 raise ValueError("KV-cached decoding does not support padding")
             with torch.no_grad():
                 return self._forward_hip_cached(x)
-        chunk = self._large_batch_chunk_size
+        chunk = self._chunk_size(x.shape[0], x.shape[1])
         with torch.no_grad():
             if chunk and x.shape[0] > chunk:
                 output = torch.empty_like(x)
@@ -408,18 +423,21 @@ class UserOptimizedTransformer(nn.Module):
         with at least one zero.
         """
         cfg = self.config
-        masked = token_valid is not None or not cfg.causal
-        if self._uses_fused_stack(x) and (not masked or cfg.head_dim <= 64):
+        plan = self.execution_plan(x.shape[0], x.shape[1], padded=token_valid is not None)
+        if not plan.runnable:
+            raise ValueError(f"no gfx950 kernel sequence for this input: {plan.forward_strategy}")
+        if plan.fused:
             wpack, ppack, affine_mask = self._fused_stack_parameters()
             return kernels.fused_forward_d128(x, wpack, ppack, cfg.num_heads, cfg.ffn_dim, len(self.layers), out=out,
                                               affine_mask=affine_mask, token_valid=token_valid, causal=cfg.causal,
+                                              split=plan.fused_variant == _capi.XB_FUSED_SPLIT,
                                               strict=self._strict_handoff_checks)
 
         def attend(index: int, layer: TransformerBlockParameters, qkv: torch.Tensor) -> torch.Tensor:
             return kernels.attention(qkv, cfg.num_heads, key_valid=token_valid, causal=cfg.causal,
-                                     scale=layer.attention.scale)
+                                     scale=layer.attention.scale, variant=plan.attention_variant)
 
-        return self._per_op_forward(x, attend, out=out, token_valid=token_valid)
+        return self._per_op_forward(x, attend, plan, out=out, token_valid=token_valid)
 
     def _forward_hip_cached(self, x: torch.Tensor) -> torch.Tensor:
         """One KV-cached step: append this chunk's keys/values per layer, attend over the cache.
@@ -455,11 +473,14 @@ class UserOptimizedTransformer(nn.Module):
             return kernels.attention_kv_cache(qkv, k_cache, v_cache, cfg.num_heads, start,
                                               scale=layer.attention.scale, workspace=workspace)
 
-        output = self._per_op_forward(x, attend)
+        plan = self.execution_plan(batch, chunk, per_op=True)
+        if not plan.runnable:
+            raise ValueError(f"no gfx950 kernel sequence for this input: {plan.forward_strategy}")
+        output = self._per_op_forward(x, attend, plan)
         self._kv_cache_length = start + chunk
         return output
 
-    def _per_op_forward(self, x: torch.Tensor, attend, out: Optional[torch.Tensor] = None,
+    def _per_op_forward(self, x: torch.Tensor, attend, plan: ShapeExecutionPlan, out: Optional[torch.Tensor] = None,
                         token_valid: Optional[torch.Tensor] = None) -> torch.Tensor:
         """LN -> per layer (QKV GEMM, attend(index, layer, qkv), out GEMM, residual LN, FFN) -> final LN."""
         cfg = self.config
@@ -477,15 +498,15 @@ class UserOptimizedTransformer(nn.Module):
             out = torch.empty_like(x)
         for index, layer in enumerate(self.layers):
             w = self._layer_weights(index)
-            qkv = kernels.linear(norm, w.qkv_w, w.qkv_b)
+            qkv = kernels.linear(norm, w.qkv_w, w.qkv_b, variant=plan.qkv_variant)
             context = attend(index, layer, qkv)
-            update = kernels.linear(context, w.out_w, w.out_b)
+            update = kernels.linear(context, w.out_w, w.out_b, variant=plan.out_variant)
             residual_in, norm2 = kernels.fused_residual_layer_norm(
                 residual_in, update, layer.norm2.weight, layer.norm2.bias, layer.norm2.eps, f16,
                 apply_affine=self._layer_norm_uses_affine(layer.norm2), residual_out=residual,
             )
-            hidden = kernels.linear(norm2, w.ffn_in_w, w.ffn_in_b, gelu=True)
-            update = kernels.linear(hidden, w.ffn_out_w, w.ffn_out_b)
+            hidden = kernels.linear(norm2, w.ffn_in_w, w.ffn_in_b, gelu=True, variant=plan.ffn_in_variant)
+            update = kernels.linear(hidden, w.ffn_out_w, w.ffn_out_b, variant=plan.ffn_out_variant)
             last = index == num_layers - 1
             following = self.final_norm if last else self.layers[index + 1].norm1
             residual_in, norm = kernels.fused_residual_layer_norm(

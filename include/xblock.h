@@ -20,7 +20,7 @@
 extern "C" {
 #endif
 
-#define XB_ABI_VERSION 2
+#define XB_ABI_VERSION 3
 
 /* Argument errors (negative); positive values are hipError_t codes. */
 #define XB_OK 0
@@ -33,6 +33,7 @@ extern "C" {
 #define XB_ERR_WORKSPACE (-7)   /* workspace_bytes below what the call needs */
 #define XB_ERR_WRONG_DEVICE (-8) /* the stream is not on the current device   */
 #define XB_ERR_SCRATCH_TOO_SMALL (-9) /* more than the static scratch holds  */
+#define XB_ERR_BAD_VARIANT (-10) /* kernel variant not built for the shape  */
 
 /* Element types of activations. */
 #define XB_F32 0
@@ -49,6 +50,44 @@ extern "C" {
 
 int xb_abi_version(void);
 const char* xb_strerror(int code);
+
+/*
+ * Execution plan.  Each op family has kernel variants; xb_select_* returns
+ * the variant the library picks for a shape (>= 0) or a negative XB_ERR_*,
+ * without touching a GPU, and the *_v entry points run a given variant
+ * (XB_VARIANT_AUTO = the selection; a variant not built for the shape gives
+ * XB_ERR_BAD_VARIANT).  The Python side turns the selections into the
+ * model's ShapeExecutionPlan and passes them back, so the plan it describes
+ * is what runs (the reference's per-shape plan, torch_transformer_benchmark.py:
+ * 98-157).  xb_variant_name(op, variant) names a variant (NULL if unknown).
+ */
+#define XB_VARIANT_AUTO (-1)
+#define XB_OP_LINEAR 0
+#define XB_OP_ATTENTION 1
+#define XB_OP_FUSED_D128 2
+/* xb_linear_v: gemm_dma_kernel tiles (K % 64 == 0, K >= 256) and gemm_nt_kernel tiles (any K % 8 == 0). */
+#define XB_LINEAR_DMA_256x256 0
+#define XB_LINEAR_DMA_256x192 1   /* also N % 192 == 0 */
+#define XB_LINEAR_DMA_128x256 2
+#define XB_LINEAR_DMA_128x128 3
+#define XB_LINEAR_NT_128x128 4
+#define XB_LINEAR_NT_64x64 5
+/* xb_attention_v: waves per block x queries per block. */
+#define XB_ATTN_W4_Q16 0     /* head_dim 256                              */
+#define XB_ATTN_W4_Q32 1     /* head_dim <= 128                           */
+#define XB_ATTN_W4_Q64 2     /* head_dim <= 64                            */
+#define XB_ATTN_W8_Q16 3     /* head_dim 256                              */
+#define XB_ATTN_PINGPONG 4   /* head_dim 64, no key mask: 512 queries      */
+/* xb_fused_forward_d128[_ws]: which form runs (the split needs a workspace). */
+#define XB_FUSED_PAIRS 0     /* one workgroup per sequence, 8 waves x 2 token blocks (head_dim <= 64) */
+#define XB_FUSED_SPLIT 1     /* two workgroups per sequence (xb_fused_forward_d128_ws)                */
+#define XB_FUSED_HD128 2     /* one workgroup per sequence, head_dim 128                             */
+const char* xb_variant_name(int op, int variant);
+int xb_select_linear(int64_t m, int32_t n, int32_t k, int epilogue);
+int xb_select_attention(int32_t batch, int64_t seq_len, int32_t heads,
+                        int32_t head_dim, int32_t masked);
+int xb_select_fused_d128(int64_t batch, int32_t seq_len, int32_t heads,
+                         int32_t ffn_dim, int32_t causal, int32_t masked);
 
 /*
  * y[r, :] = LayerNorm(x[r, :]) (* gamma + beta when apply_affine), FP32 math,
@@ -101,6 +140,10 @@ int xb_residual_layernorm_masked(const float* residual, const void* update,
  */
 int xb_linear(const void* a, const void* w, const float* bias, void* c,
               int64_t m, int32_t n, int32_t k, int epilogue, void* stream);
+/* xb_linear running a given tile variant (XB_LINEAR_*, or XB_VARIANT_AUTO). */
+int xb_linear_v(const void* a, const void* w, const float* bias, void* c,
+                int64_t m, int32_t n, int32_t k, int epilogue, int variant,
+                void* stream);
 
 /*
  * Causal multi-head attention over a packed projection.
@@ -126,6 +169,11 @@ int xb_attention_causal(const void* qkv, void* out, int32_t batch,
 int xb_attention(const void* qkv, void* out, const uint8_t* key_valid,
                  int32_t batch, int64_t seq_len, int32_t heads,
                  int32_t head_dim, float scale, int32_t causal, void* stream);
+/* xb_attention running a given kernel variant (XB_ATTN_*, or XB_VARIANT_AUTO). */
+int xb_attention_v(const void* qkv, void* out, const uint8_t* key_valid,
+                   int32_t batch, int64_t seq_len, int32_t heads,
+                   int32_t head_dim, float scale, int32_t causal, int variant,
+                   void* stream);
 
 /*
  * KV cache for incremental causal decoding (replaces _append_kv_cache and the

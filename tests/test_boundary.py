@@ -41,12 +41,58 @@ def test_benchmark_configs_match_baseline_json(pkg):
     assert "B=10000" in configs[1] and "head_dim 8" in configs[3] and "S=100000" in configs[4]
 
 
-def test_shape_plan(pkg):
-    plan = pkg.resolve_shape_execution_plan(pkg.OFFICIAL_BENCHMARK_SHAPES[6])
+def test_shape_plan(pkg, capi):
+    """The plan is the library's selection (no GPU needed) and names what runs."""
+    shapes = pkg.OFFICIAL_BENCHMARK_SHAPES
+    plan = pkg.resolve_shape_execution_plan(shapes[6])
     assert plan.official_shape_id == 6
     assert plan.describe().startswith("official-6: ffn=")
+    assert plan.fused and plan.fused_variant == capi.XB_FUSED_PAIRS and plan.batch_chunk_size == 0
+    assert "fused_stack_1wg_8wave_pairs" in plan.describe()
+    # small causal batches split each sequence over two workgroups
+    for shape_id in (1, 11):
+        assert pkg.resolve_shape_execution_plan(shapes[shape_id]).fused_variant == capi.XB_FUSED_SPLIT
+    # D=1024: per-op kernels; the QKV GEMM's tile is the cost model's (256 x 192 for N = 3072)
+    cfg3 = pkg.resolve_shape_execution_plan(shapes[8])
+    assert not cfg3.fused and cfg3.qkv_variant == 1 and "mfma_gemm_dma_256x192" in cfg3.projection_strategy
+    assert cfg3.attention_strategy == "flash_8wave_128q"
+    cfg5 = pkg.resolve_shape_execution_plan(shapes[14])
+    assert cfg5.attention_strategy == "flash_pingpong_8wave_512q" and cfg5.batch_chunk_size == 0
+    # a padded mask takes the key-masked forms: no ping-pong kernel
+    assert pkg.resolve_shape_execution_plan(shapes[14], masked=True).attention_strategy == "flash_4wave_256q"
+    # the whole-stack kernel off (toggle or LayerNorm contract): per-op
+    assert not pkg.resolve_shape_execution_plan(shapes[6], fused_allowed=False).fused
+    # a batch beyond the HBM budget runs in slices
+    big = pkg.TransformerConfig(400, 100000, 1024, 16, 1024, 2, True)
+    chunked = pkg.resolve_shape_execution_plan(big)
+    assert 0 < chunked.batch_chunk_size < 400 and "batch_chunk=" in chunked.describe()
     general = pkg.resolve_shape_execution_plan(pkg.TransformerConfig(3, 5, 8, 2, 8, 1, True))
     assert general.official_shape_id is None and general.describe().startswith("general:")
+
+
+def test_variant_selection_abi(capi):
+    """xb_select_* and the *_v entry points' variant checks need no GPU."""
+    lib = capi.lib()
+    assert lib.xb_select_linear(8192, 3072, 1024, 0) == 1          # 256 x 192
+    assert lib.xb_select_linear(8192, 384, 128, 0) in (4, 5)       # K = 128: the nt kernel
+    assert lib.xb_select_linear(-1, 8, 8, 0) == -2
+    assert lib.xb_select_attention(64, 128, 4, 256, 0) == 3          # cfg3: one 8-wave block per (batch, head)
+    assert lib.xb_select_attention(8, 128, 4, 256, 0) == 0           # too few blocks for that
+    assert lib.xb_select_attention(32, 100000, 16, 64, 0) == 4
+    assert lib.xb_select_attention(32, 100000, 16, 64, 1) == 2
+    assert lib.xb_select_attention(1, 8, 2, 24, 0) == -4
+    assert lib.xb_select_fused_d128(64, 128, 4, 128, 1, 0) == 1
+    assert lib.xb_select_fused_d128(10000, 128, 4, 128, 1, 0) == 0
+    assert lib.xb_select_fused_d128(8, 128, 1, 128, 1, 1) == -4    # head_dim 128: causal, unmasked only
+    assert lib.xb_select_fused_d128(8, 129, 4, 128, 1, 0) == -4
+    # a variant not built for the shape is refused before any launch
+    assert lib.xb_linear_v(16, 16, None, 16, 8192, 384, 128, 0, 0, None) == -10      # DMA tile needs K >= 256
+    assert lib.xb_linear_v(16, 16, None, 16, 8192, 1024, 1024, 0, 1, None) == -10    # 256 x 192 needs N % 192
+    assert lib.xb_attention_v(16, 16, None, 2, 64, 2, 32, 0.1, 1, 4, None) == -10     # ping-pong: head_dim 64 only
+    assert lib.xb_attention_v(16, 16, 16, 2, 64, 2, 64, 0.1, 1, 4, None) == -10       # nor with a key mask
+    names = {lib.xb_variant_name(op, v) for op, n in ((0, 6), (1, 5), (2, 3)) for v in range(n)}
+    assert None not in names and len(names) == 14
+    assert lib.xb_variant_name(0, 99) is None
 
 
 @pytest.mark.parametrize("geom", [(2, 8, 32, 4, 48, 2), (1, 4, 128, 16, 128, 1)])
@@ -103,13 +149,14 @@ def test_tree_cache_follows_registrations(pkg):
     params, norms = model._tree()
     assert list(params) == list(model.parameters()) and len(norms) == 2 * 2 + 1
     assert model._tree()[0] is params                      # no registration: the same walk
-    assert model._uses_fused_stack(x) and not model._single_launch_forward(x, None)  # CPU input
+    assert model._fused_stack_eligible() and not model._single_launch_forward(x, None)  # CPU input
     fresh = torch.nn.Parameter(torch.zeros(128, 128))
     model.layers[1].ffn_in.weight = fresh
     assert any(p is fresh for p in model._tree()[0])
     model.final_norm = torch.nn.LayerNorm(128, eps=1e-6)
     assert model._tree()[1][-1] is model.final_norm
-    assert not model._uses_fused_stack(x)                  # eps outside the kernel's contract
+    assert not model._fused_stack_eligible()               # eps outside the kernel's contract
+    assert not model.execution_plan(2, 8).fused
 
 
 def test_product_never_touches_the_oracle():

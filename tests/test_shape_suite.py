@@ -37,8 +37,9 @@ def test_peak_estimate_scales_with_tokens(pkg):
 
 
 def _line(value=1e6, failed=0, passed=True):
-    return json.dumps({"value": value, "ms_per_step": 1.5, "roofline_frac_forward": 0.25, "bound_forward": "hbm",
-                       "roofline_frac_forward_min": 0.04, "bound_forward_min": "mfma",
+    return json.dumps({"value": value, "ms_per_step": 1.5,
+                       "roofline": {"kernel": "fused_forward_d128", "bound": "hbm", "frac": 0.25},
+                       "forward_roofline": {"bound": "mfma", "frac": 0.04},
                        "accuracy": {"failed": failed, "total": 100, "passed": passed, "trials": 2},
                        "cpu_baseline": {"value": 1e3}})
 
@@ -80,6 +81,11 @@ def test_statuses_summary_and_exit_codes(pkg):
     assert 8 not in [int(c[c.index("--workload") + 1]) for c in launcher.commands]
     cmd14 = launcher.commands[3]
     assert cmd14[cmd14.index("--batch") + 1] == "4" and "--strict-accuracy" in cmd14
+    # bench.py's own guard (SAFE_SKIP / SAFE_ABORT, status 3) is a SKIP with its reason
+    launcher.outcomes[11] = (3, "SAFE_ABORT: out of device memory: HIP out of memory\n")
+    skipped = suite.run_suite([11], shapes, args, None, launcher)[0]
+    assert skipped.status == "SKIP" and skipped.reason.startswith("SAFE_ABORT")
+    launcher.commands.pop()
     assert suite.exit_status(results, strict=False) == 1
     ok = [by_id[1], by_id[14]]
     assert suite.exit_status(ok, strict=False) == 0
