@@ -563,21 +563,33 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
     asm volatile("" : "+v"(ql), "+v"(kc), "+v"(kr));
     const half_t* kt_lds = k_lds[t & (NBUF - 1)];
     const half_t* kp[KSTEPS] = {kt_lds + kr + 8 * kc, kt_lds + kr + 8 * (kc ^ 4)};
+    // K fragments run two key blocks ahead of their products, in two slots
+    // (a slot is refilled right after the products that read it issue).
+    half8_t kf[2][KSTEPS];
+    auto read_k = [&](int jb) {
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks) kf[jb % 2][ks] = *reinterpret_cast<const half8_t*>(kp[ks] + 16 * jb * ROW);
+    };
+    read_k(0);
     half8_t qf[NQ][KSTEPS];
 #pragma unroll
     for (int qb = 0; qb < NQ; ++qb)
 #pragma unroll
       for (int ks = 0; ks < KSTEPS; ++ks) qf[qb][ks] = q_lds[wave][qb][ks][ql];
+    read_k(1);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int jb = 0; jb < KB; ++jb) {
+    for (int jb = 0; jb < KB; ++jb)
 #pragma unroll
       for (int qb = 0; qb < NQ; ++qb) s[jb][qb] = float4_t{-m_run[qb], -m_run[qb], -m_run[qb], -m_run[qb]};
 #pragma unroll
-      for (int ks = 0; ks < KSTEPS; ++ks) {
-        const half8_t kf = *reinterpret_cast<const half8_t*>(kp[ks] + 16 * jb * ROW);
+    for (int jb = 0; jb < KB; ++jb) {
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int qb = 0; qb < NQ; ++qb) s[jb][qb] = mfma16x16x32(kf, qf[qb][ks], s[jb][qb]);
-      }
+      for (int ks = 0; ks < KSTEPS; ++ks)
+#pragma unroll
+        for (int qb = 0; qb < NQ; ++qb) s[jb][qb] = mfma16x16x32(kf[jb % 2][ks], qf[qb][ks], s[jb][qb]);
+      if (jb + 2 < KB) read_k(jb + 2);
     }
   };
   // O^T += V^T . P^T of tile t (and the row sums).
@@ -588,20 +600,32 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
     int vr = (4 * g + r16 / 4) * ROW + 4 * (r16 % 2), cb = ((r16 % 4) / 2) ^ ((4 * g + r16 / 4) & 7);
     asm volatile("" : "+v"(vr), "+v"(cb));
     const half_t* vt_lds = v_lds[t % NBUF] + vr;
+    // V fragments run two steps (4 kt + hb) ahead of their products in a
+    // ring of three; the row-sum products, which read no LDS, go first and
+    // cover the first two reads.  The sched_barriers keep that order.
+    half8_t vf[3];
+    auto read_v = [&](int step) {
+      const int kt = step / HB, hb = step % HB;
+      const half_t* vrow = vt_lds + 32 * kt * ROW;
+      const int slot = 8 * (cb ^ (2 * hb));
+      const half4_t lo = lds_read_tr16(vrow + slot);
+      const half4_t hi = lds_read_tr16(vrow + 16 * ROW + slot);
+      vf[step % 3] = half8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    };
+    read_v(0);
+    read_v(1);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int kt = 0; kt < KT; ++kt) {
+    for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
       for (int qb = 0; qb < NQ; ++qb) lacc[qb] = mfma16x16x32(ones8, pf[kt][qb], lacc[qb]);
-      const half_t* vrow = vt_lds + 32 * kt * ROW;
 #pragma unroll
-      for (int hb = 0; hb < HB; ++hb) {
-        const int slot = 8 * (cb ^ (2 * hb));
-        const half4_t lo = lds_read_tr16(vrow + slot);
-        const half4_t hi = lds_read_tr16(vrow + 16 * ROW + slot);
-        const half8_t vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    for (int step = 0; step < KT * HB; ++step) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (step + 2 < KT * HB) read_v(step + 2);
+      const int kt = step / HB, hb = step % HB;
 #pragma unroll
-        for (int qb = 0; qb < NQ; ++qb) o[hb][qb] = mfma16x16x32(vf, pf[kt][qb], o[hb][qb]);
-      }
+      for (int qb = 0; qb < NQ; ++qb) o[hb][qb] = mfma16x16x32(vf[step % 3], pf[kt][qb], o[hb][qb]);
     }
   };
   // Mask, offset check / rescale, probabilities of tile t.
