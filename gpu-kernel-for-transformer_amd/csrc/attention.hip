@@ -497,13 +497,13 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
     }
   }
   float4_t o[HB][NQ], lacc[NQ];
-  float m_run[NQ];
+  float4_t minit[NQ];  // -m_run broadcast: the score accumulators' start value
 #pragma unroll
   for (int qb = 0; qb < NQ; ++qb) {
 #pragma unroll
     for (int hb = 0; hb < HB; ++hb) o[hb][qb] = float4_t{0.f, 0.f, 0.f, 0.f};
     lacc[qb] = float4_t{0.f, 0.f, 0.f, 0.f};
-    m_run[qb] = 0.f;
+    minit[qb] = float4_t{0.f, 0.f, 0.f, 0.f};
   }
   const half8_t ones8 = {1, 1, 1, 1, 1, 1, 1, 1};
 
@@ -579,16 +579,13 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
     read_k(1);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int jb = 0; jb < KB; ++jb)
-#pragma unroll
-      for (int qb = 0; qb < NQ; ++qb) s[jb][qb] = float4_t{-m_run[qb], -m_run[qb], -m_run[qb], -m_run[qb]};
-#pragma unroll
     for (int jb = 0; jb < KB; ++jb) {
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int ks = 0; ks < KSTEPS; ++ks)
 #pragma unroll
-        for (int qb = 0; qb < NQ; ++qb) s[jb][qb] = mfma16x16x32(kf[jb % 2][ks], qf[qb][ks], s[jb][qb]);
+        for (int qb = 0; qb < NQ; ++qb)
+          s[jb][qb] = mfma16x16x32(kf[jb % 2][ks], qf[qb][ks], ks == 0 ? minit[qb] : s[jb][qb]);
       if (jb + 2 < KB) read_k(jb + 2);
     }
   };
@@ -678,7 +675,7 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
         // jumps there with nothing to rescale; later sh >= 0 and corr <= 1.
         const float sh = t != 0 ? fmaxf(mx, 0.f) : mx;
         const float corr = t != 0 ? __builtin_amdgcn_exp2f(-sh) : 1.f;
-        m_run[qb] += sh;
+        minit[qb] -= sh;
 #pragma unroll
         for (int hb = 0; hb < HB; ++hb) o[hb][qb] *= corr;
         lacc[qb] *= corr;
