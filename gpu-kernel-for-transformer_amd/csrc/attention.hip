@@ -149,23 +149,21 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_kernel(const AttnArgs a)
 
   // Q fragments (B operand of S^T), pre-multiplied by scale * log2(e):
   // lane holds q[query][32*ks + 8*(l/16) .. +7].
+  // Loaded unconditionally (outside the query range or past HD the lane
+  // reads row 0, column 0 and zeroes the fragment afterwards), so every load
+  // is in flight at once instead of one conditional load and wait per
+  // fragment; scaled after the first K/V tile has been requested.
   half8_t qf[NQ][KSTEPS];
   const half8_t zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
+  auto q_ok = [&](int qb, int ks) { return qw0 + 16 * qb + r16 < S_q && 32 * ks + 8 * g < HD; };
 #pragma unroll
-  for (int qb = 0; qb < NQ; ++qb) {
-    const int q = qw0 + 16 * qb + r16;
+  for (int qb = 0; qb < NQ; ++qb)
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) {
-      const int d = 32 * ks + 8 * g;
-      half8_t v = zero8;
-      if (q < S_q && d < HD) {
-        v = *reinterpret_cast<const half8_t*>(base + q * q_rstride + d);
-#pragma unroll
-        for (int m = 0; m < 8; ++m) v[m] = (half_t)((float)v[m] * scale_log2);
-      }
-      qf[qb][ks] = v;
+      const bool ok = q_ok(qb, ks);
+      const int q = ok ? qw0 + 16 * qb + r16 : 0, d = ok ? 32 * ks + 8 * g : 0;
+      qf[qb][ks] = *reinterpret_cast<const half8_t*>(base + q * q_rstride + d);
     }
-  }
 
   // m_run: the base-2 exponent offset of query (l % 16) of block qb.  The score
   // MFMAs start from -m_run, so a tile's scores arrive already shifted; the
@@ -239,6 +237,15 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_kernel(const AttnArgs a)
     gload(k_begin);
     sstore(0);
   }
+#pragma unroll
+  for (int qb = 0; qb < NQ; ++qb)
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+      half8_t v = qf[qb][ks];
+#pragma unroll
+      for (int m = 0; m < 8; ++m) v[m] = (half_t)((float)v[m] * scale_log2);
+      qf[qb][ks] = q_ok(qb, ks) ? v : zero8;
+    }
   __syncthreads();
   for (int t = 0; t < n_tiles; ++t) {
     const int cur = NBUF == 1 ? 0 : t & 1;
