@@ -45,6 +45,17 @@ XB_OP_FUSED_D128 = 2
 XB_FUSED_PAIRS = 0
 XB_FUSED_SPLIT = 1
 XB_FUSED_HD128 = 2
+XB_LINEAR_DMA_256x256 = 0
+XB_LINEAR_DMA_256x192 = 1
+XB_LINEAR_DMA_128x256 = 2
+XB_LINEAR_DMA_128x128 = 3
+XB_LINEAR_NT_128x128 = 4
+XB_LINEAR_NT_64x64 = 5
+XB_ATTN_W4_Q16 = 0
+XB_ATTN_W4_Q32 = 1
+XB_ATTN_W4_Q64 = 2
+XB_ATTN_W8_Q16 = 3
+XB_ATTN_PINGPONG = 4
 
 EXPORTED_SYMBOLS = (
     "xb_abi_version",

@@ -98,6 +98,29 @@ def test_linear(pkg, cuda, m, n, k, gelu):
     torch.testing.assert_close(out.cpu().float(), ref, atol=2e-3, rtol=2e-3)
 
 
+@pytest.mark.parametrize("m,n,k", [(1000, 1152, 1024), (300, 384, 256), (8192, 768, 512)])
+@pytest.mark.parametrize("gelu", [False, True])
+def test_linear_every_variant(pkg, cuda, m, n, k, gelu):
+    """Every tile variant the plan can name (xb_linear_v), forced on shapes all
+    of them accept, against the FP32 reference; a variant not built for the
+    shape is refused."""
+    capi = pkg._capi
+    a = torch.randn(m, k, generator=_gen(m + k)).half()
+    w = (torch.randn(n, k, generator=_gen(n)) * k**-0.5).half()
+    bias = torch.randn(n, generator=_gen(k)) * 0.1
+    ref = a.float() @ w.float().T + bias
+    if gelu:
+        ref = F.gelu(ref, approximate="none")
+    ag, wg, bg = a.to(cuda), w.to(cuda), bias.to(cuda)
+    for variant in (capi.XB_LINEAR_DMA_256x256, capi.XB_LINEAR_DMA_256x192, capi.XB_LINEAR_DMA_128x256,
+                    capi.XB_LINEAR_DMA_128x128, capi.XB_LINEAR_NT_128x128, capi.XB_LINEAR_NT_64x64):
+        out = pkg.linear(ag, wg, bg, gelu=gelu, variant=variant)
+        torch.testing.assert_close(out.cpu().float(), ref, atol=2e-3, rtol=2e-3,
+                                   msg=lambda e, v=variant: f"variant {v}: {e}")
+    with pytest.raises(RuntimeError, match="code -10"):  # 256x192 needs N % 192 == 0
+        pkg.linear(ag[:, :k], wg[:n - 128], None, variant=capi.XB_LINEAR_DMA_256x192)
+
+
 def test_linear_without_bias_and_batched_shape(pkg, cuda):
     a = torch.randn(3, 5, 64, generator=_gen(1)).half()
     w = (torch.randn(32, 64, generator=_gen(2)) * 0.125).half()
@@ -168,6 +191,30 @@ def test_attention_long_hd64_ping_pong(pkg, cuda, b, s, h, causal):
     torch.testing.assert_close(out.cpu().float(), ref, atol=2e-3, rtol=1e-2)
     ones = torch.ones(b, s, dtype=torch.bool, device=cuda)
     assert torch.equal(out, pkg.attention(qg, h, key_valid=ones, causal=causal))
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("hd,b,s,h,variants", [
+    (256, 2, 300, 2, ("XB_ATTN_W4_Q16", "XB_ATTN_W8_Q16")),
+    (128, 1, 333, 2, ("XB_ATTN_W4_Q32",)),
+    (64, 2, 4100, 1, ("XB_ATTN_W4_Q32", "XB_ATTN_W4_Q64", "XB_ATTN_PINGPONG")),
+    (32, 1, 1100, 3, ("XB_ATTN_W4_Q32", "XB_ATTN_W4_Q64")),
+])
+def test_attention_every_variant(pkg, cuda, causal, hd, b, s, h, variants):
+    """Every attention kernel the plan can name (xb_attention_v), forced on a
+    shape it is built for, against the FP32 reference; the ping-pong kernel is
+    refused under a key mask."""
+    capi = pkg._capi
+    qkv = torch.randn(b, s, 3 * h * hd, generator=_gen(hd + s)).half()
+    ref = _attention_reference(qkv, h, causal=causal)
+    qg = qkv.to(cuda)
+    for name in variants:
+        out = pkg.attention(qg, h, causal=causal, variant=getattr(capi, name))
+        torch.testing.assert_close(out.cpu().float(), ref, atol=2e-3, rtol=1e-2, msg=lambda e, n=name: f"{n}: {e}")
+    if hd == 64:
+        ones = torch.ones(b, s, dtype=torch.bool, device=cuda)
+        with pytest.raises(RuntimeError, match="code -10"):
+            pkg.attention(qg, h, key_valid=ones, causal=causal, variant=capi.XB_ATTN_PINGPONG)
 
 
 @pytest.mark.parametrize("causal", [True, False])
