@@ -439,11 +439,11 @@ __device__ __forceinline__ void dma16_untracked(const void* src_lane, void* lds_
 // wave keeps the matrix core busy while the other issues the exponentials,
 // instead of both waves reaching the same phase at once.
 //
-// K/V tiles sit in a ring of three LDS buffers (tile t in buffer t % 3) and
+// K/V tiles sit in a ring of four LDS buffers (tile t in buffer t % 4) and
 // arrive by direct global -> LDS loads (no VGPRs in between).  Tile t is read
-// from half-step 2t (A's QK) to 2t+3 (B's PV); the loads of tile t+1 are
+// from half-step 2t (A's QK) to 2t+3 (B's PV); the loads of tile t+2 are
 // issued in half-step 2t (into the buffer of tile t-2, last read in 2t-1) and
-// waited for at the end of 2t+1.  Rows are 128 bytes, unpadded
+// waited for at the end of 2t+3.  Rows are 128 bytes, unpadded
 // (a load fills 1 KB = 8 rows contiguously); chunk c of row r sits in slot
 // c ^ (r & 7), applied on the global side, which keeps the K fragment reads
 // and the transposing V reads free of bank conflicts.  Same arithmetic as
