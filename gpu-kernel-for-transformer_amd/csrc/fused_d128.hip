@@ -793,7 +793,8 @@ __device__ __forceinline__ void fetch_kv(Lds& L, const SplitExchange& ex, int64_
 // per sequence).  NBT = 1 with SPLIT: two workgroups per sequence, `part` 0
 // holding blocks 0-3 and part 1 blocks 4-7, one block (pair + 4 part) and one
 // feature half per wave; part 0 publishes each layer's K and V^T of tokens
-// 0..63 to `ex` and part 1 fetches them before its attention.
+// 0..63 to `ex` as soon as they are in LDS (before its Q projection) and
+// part 1 fetches them after its own Q projection, just before attention.
 template <int HD, int HALF, int MASK, int NBT, bool SPLIT>
 __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ x, float* __restrict__ y,
                                               const half_t* __restrict__ wpack, const float* __restrict__ ppack,
@@ -823,9 +824,13 @@ __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ 
     tb[0] = 4 * part + pair;
   }
 
+  // A layer's groups are consumed in the order K, V, Q, O, W1, W2 (the
+  // packed buffer holds Q, K, V, O, W1, W2): K and V^T are then in LDS one
+  // stage before Q, so the split form publishes them while Q is computed.
   auto issue_group = [&](int gi) {
     const int layer = gi / MATS, m = gi % MATS;
-    const half_t* src = wpack + ((int64_t)layer * MATS + m) * MAT_FRAGS * 512;
+    const int mat = m < 3 ? (m + 1) % 3 : m;
+    const half_t* src = wpack + ((int64_t)layer * MATS + mat) * MAT_FRAGS * 512;
 #pragma unroll
     for (int j = 0; j < MAT_FRAGS / NW; ++j) {
       const int f = wave + NW * j;
@@ -867,28 +872,13 @@ __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ 
       half8_t own[NBT][OK];
       split_layer_norm2(res, pp + P_G1, pp + P_BE1, (affine_mask >> min(2 * layer, 63)) & 1, xstat[0], wave, lane,
                         half, g, own);
-      put_half2(area_a, own, xn, tb, half, lane);
+      put_half2(area_b, own, xn, tb, half, lane);  // area_a is K's: K is written first
     }
 
-    // ---- Q (own heads), kept in registers --------------------------------
-    half8_t qop[NBT][OK];
-    {
-      const char* st = begin_group(g0 + 0);
-      get_partner2(area_a, xn, tb, half, lane);
-      float4_t qc[NBT][OB];
-#pragma unroll
-      for (int b = 0; b < NBT; ++b)
-#pragma unroll
-        for (int j = 0; j < OB; ++j) qc[b][j] = ld4(pp + P_BQ + 16 * (OB * half + j) + 4 * g);
-      stage_gemm2<true>(st, xn, qc, half, lane);
-#pragma unroll
-      for (int b = 0; b < NBT; ++b)
-#pragma unroll
-        for (int j = 0; j < OK; ++j) qop[b][j] = to_operand(qc[b][2 * j], qc[b][2 * j + 1]);
-    }
     // ---- K (own features) -> LDS, permuted per k-step ----------------------
     {
-      const char* st = begin_group(g0 + 1);
+      const char* st = begin_group(g0 + 0);
+      get_partner2(area_b, xn, tb, half, lane);
       float4_t a[NBT][OB];
 #pragma unroll
       for (int b = 0; b < NBT; ++b)
@@ -904,9 +894,9 @@ __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ 
               to_half4(a[b][j]);
         }
     }
-    // ---- V (own features) -> V^T in LDS -------------------------------------
+    // ---- V (own features) -> V^T in LDS (after every wave has read area_b) --
     {
-      const char* st = begin_group(g0 + 2);
+      const char* st = begin_group(g0 + 1);
       float4_t a[NBT][OB];
 #pragma unroll
       for (int j = 0; j < OB; ++j) {
@@ -922,12 +912,27 @@ __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ 
           *reinterpret_cast<half4_t*>(vt_lds + (16 * (OB * half + j) + r16) * LD + 16 * tb[b] + 4 * g) =
               to_half4(a[b][j]);
     }
-    lds_barrier();  // K and V^T of every token block are in LDS
+    // ---- Q (own heads), kept in registers --------------------------------
+    // The group's barrier also puts K and V^T of every token block in LDS.
+    half8_t qop[NBT][OK];
+    {
+      const char* st = begin_group(g0 + 2);
+      if constexpr (SPLIT) {
+        if (part == 0) publish_kv(L, ex, seq, layer, epoch);
+      }
+      float4_t qc[NBT][OB];
+#pragma unroll
+      for (int b = 0; b < NBT; ++b)
+#pragma unroll
+        for (int j = 0; j < OB; ++j) qc[b][j] = ld4(pp + P_BQ + 16 * (OB * half + j) + 4 * g);
+      stage_gemm2<true>(st, xn, qc, half, lane);
+#pragma unroll
+      for (int b = 0; b < NBT; ++b)
+#pragma unroll
+        for (int j = 0; j < OK; ++j) qop[b][j] = to_operand(qc[b][2 * j], qc[b][2 * j + 1]);
+    }
     if constexpr (SPLIT) {
-      if (part == 0)
-        publish_kv(L, ex, seq, layer, epoch);
-      else
-        fetch_kv(L, ex, seq, layer, epoch);
+      if (part == 1) fetch_kv(L, ex, seq, layer, epoch);
     }
 
     // ---- causal attention of both blocks, own heads --------------------------
