@@ -600,7 +600,9 @@ __device__ __forceinline__ void stage_gemm2(const char* st, const half8_t (&act)
 // Row statistics of both blocks from both halves, one barrier for the two:
 // each wave's (mean, M2) over its 64 features meet in LDS and merge by Chan's
 // pairwise formula (equal counts: M2 = M2a + M2b + (ma - mb)^2 * 32); both
-// waves of a pair get bit-identical results (the merge is symmetric).
+// waves of a pair get bit-identical results (the merge is symmetric).  The
+// wave holding the other half of the same blocks is w ^ 4 in the pair form
+// (NBT = 2) and 7 - w in the split form (see stack8x2_body).
 template <int NBT>
 __device__ __forceinline__ void split_row_stats2(const float4_t (&r)[NBT][OB], float2* xs, int wave, int lane,
                                                  float (&mean)[NBT], float (&rstd)[NBT]) {
@@ -627,7 +629,7 @@ __device__ __forceinline__ void split_row_stats2(const float4_t (&r)[NBT][OB], f
   lds_barrier();
 #pragma unroll
   for (int b = 0; b < NBT; ++b) {
-    const float2 pb = xs[((wave ^ 4) * NBT + b) * 16 + l % 16];
+    const float2 pb = xs[((NBT == 2 ? wave ^ 4 : 7 - wave) * NBT + b) * 16 + l % 16];
     const float d = pb.x - ma[b];
     mean[b] = 0.5f * (ma[b] + pb.x);
     rstd[b] = __builtin_amdgcn_rsqf(((m2a[b] + pb.y) + d * d * 32.f) * (1.0f / D) + 1e-5f);
@@ -767,8 +769,11 @@ __device__ __forceinline__ void fetch_kv(Lds& L, const SplitExchange& ex, int64_
   unsigned long long* flag = ex.flags + seq * ex.layers + layer;
   const int t = threadIdx.x;
   if (t == 0) {
+    // Poll with relaxed loads and acquire once after the loop: an acquiring
+    // load invalidates this XCD's L2 on every poll, evicting the weights the
+    // other workgroups there are reading.
     int spins = 0;
-    while (__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) != epoch) {
+    while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != epoch) {
       if (spins >= ex.spin_limit) {
         atomicAdd(&ex.hdr->errors, 1);
         L.poison = 1;
@@ -777,6 +782,7 @@ __device__ __forceinline__ void fetch_kv(Lds& L, const SplitExchange& ex, int64_
       __builtin_amdgcn_s_sleep(1);
       ++spins;
     }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
   __syncthreads();
 #pragma unroll
@@ -791,10 +797,14 @@ __device__ __forceinline__ void fetch_kv(Lds& L, const SplitExchange& ex, int64_
 
 // NBT = 2: the pair form above (blocks pair, 7 - pair per wave, one workgroup
 // per sequence).  NBT = 1 with SPLIT: two workgroups per sequence, `part` 0
-// holding blocks 0-3 and part 1 blocks 4-7, one block (pair + 4 part) and one
-// feature half per wave; part 0 publishes each layer's K and V^T of tokens
-// 0..63 to `ex` as soon as they are in LDS (before its Q projection) and
-// part 1 fetches them after its own Q projection, just before attention.
+// holding blocks 0-3 and part 1 blocks 4-7, one block and one feature half
+// per wave: wave w < 4 takes half 0 of block 4 part + w, wave w + 4 half 1 of
+// block 4 part + 3 - w, so the two waves of a SIMD see 8 part + 5 key blocks
+// between them, the same on every SIMD (the waves holding the two halves of
+// one block, w and 7 - w, sit on different SIMDs); part 0 publishes each
+// layer's K and V^T of tokens 0..63 to `ex` as soon as they are in LDS
+// (before its Q projection) and part 1 fetches them after its own Q
+// projection, just before attention.
 template <int HD, int HALF, int MASK, int NBT, bool SPLIT>
 __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ x, float* __restrict__ y,
                                               const half_t* __restrict__ wpack, const float* __restrict__ ppack,
@@ -821,7 +831,7 @@ __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ 
     tb[0] = pair;
     tb[1] = 7 - pair;
   } else {
-    tb[0] = 4 * part + pair;
+    tb[0] = 4 * part + (HALF == 0 ? pair : 3 - pair);
   }
 
   // A layer's groups are consumed in the order K, V, Q, O, W1, W2 (the
@@ -1109,7 +1119,7 @@ __global__ __launch_bounds__(64 * NW, 1) void fused_split_kernel(
       lds.kval[t] = t < S && (token_valid == nullptr || token_valid[seq * S + t] != 0) ? 1 : 0;
   }
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int pair = wave % 4;  // block 4 part + pair; waves w and w + 4 (its two halves) share a SIMD
+  const int pair = wave % 4;  // waves w and w + 4 share a SIMD (block assignment: stack8x2_body)
   if (wave < 4)
     stack8x2_body<HD, 0, MASK, 1, true>(lds, x, y, wpack, ppack, S, layers, affine_mask, wave, pair, seq, part, ex,
                                          epoch);
