@@ -702,31 +702,42 @@ __device__ __forceinline__ void attend_pair(const Lds& L, const half8_t (&qop)[N
 
 // K/V exchange of the split form.  Per (sequence, layer) a 32 KB slot: K rows
 // of tokens 0..63 ([64][128] halves) then their V^T columns ([128][64]), and
-// a 64-bit flag.  Every launch has its own epoch, the workspace's generation
-// plus one: part 0 stores the slot and then the epoch into the flag (release,
-// agent scope); part 1 waits until the flag holds this launch's epoch
-// (acquire) and copies the slot into its LDS.  A flag left by an earlier
-// launch holds an older epoch and never satisfies a later wait, so nothing
-// has to be lowered again and a late producer cannot feed the next call.  The
-// last block of the grid to finish (a counter of finished blocks) advances the
+// a 64-bit flag holding (epoch << 4) | the producer's XCD.  Every launch has
+// its own epoch, the workspace's generation plus one: part 0 stores the slot
+// and then the flag; part 1 waits until the flag holds this launch's epoch
+// and copies the slot into its LDS.  A flag left by an earlier launch holds
+// an older epoch and never satisfies a later wait, so nothing has to be
+// lowered again and a late producer cannot feed the next call.  The last
+// block of the grid to finish (a counter of finished blocks) advances the
 // generation; the next launch on the stream starts after this one has ended,
 // so every block of a launch reads the same generation.
 //
-// Forward progress: part 1 of sequence b only waits on part 0 of b.  The host
-// places them on one XCD (blocks b and R + b with R a multiple of the eight
-// XCDs, which receive blocks round-robin) where part 0 has the lower index, so
-// that XCD's in-order dispatcher started part 0 first; part 0 never waits.
-// The wait is still bounded (spin_limit sleeps): a wait that runs out counts
-// an error in the header, poisons the block (its output rows become NaN) and
-// goes on, so every wave of the grid ends.
+// Placement: the host puts both parts of sequence b on one XCD (blocks b and
+// R + b with R a multiple of the eight XCDs, which receive blocks
+// round-robin), so the slot goes through that XCD's L2 only, the point where
+// all of its CUs' accesses meet: the producer's stores are acknowledged by
+// the L2 (vmcnt(0)) before the flag is stored, and the consumer's plain loads
+// after it sees the flag miss its L1 (the slot is read once per launch, and
+// every kernel starts with clean L1s) and read the L2.  So neither an L2
+// write-back (agent-scope release) nor an L2 invalidate (agent-scope
+// acquire) is needed; both stall the XCD, 6% of cfg1's time.  The consumer
+// checks the XCD id in the flag against its own, so a placement that ever
+// differed would be counted and poisoned like a time-out, never read.
+//
+// Forward progress: part 1 of sequence b only waits on part 0 of b, which
+// has the lower index on the same XCD, so that XCD's in-order dispatcher
+// started it first; part 0 never waits.  The wait is still bounded
+// (spin_limit sleeps): a wait that runs out counts an error in the header,
+// poisons the block (its output rows become NaN) and goes on, so every wave
+// of the grid ends.
 struct SplitHeader {
-  int errors;                      // hand-offs that timed out, over all launches
+  int errors;                      // failed hand-offs (timed out, or across XCDs), over all launches
   unsigned done;                   // blocks of the current launch that finished
   unsigned long long generation;   // launches completed on this workspace
 };
 struct SplitExchange {
   half_t* kv;                      // [batch][layers][2][64 * 128]
-  unsigned long long* flags;       // [kSplitMaxBatch][layers]: epoch of the last publish
+  unsigned long long* flags;       // [kSplitMaxBatch][layers]: (epoch << 4) | XCD of the last publish
   SplitHeader* hdr;
   int layers;
   int spin_limit;                  // sleeps before a wait gives up
@@ -747,6 +758,9 @@ __device__ __forceinline__ void split_block_done(const SplitExchange& ex, unsign
   }
 }
 
+// The XCD (0..7) this wave runs on.
+__device__ __forceinline__ unsigned xcd_id() { return __builtin_amdgcn_s_getreg((3 << 11) | 20) & 15u; }  // HW_REG_XCC_ID[3:0]
+
 __device__ __forceinline__ void publish_kv(const Lds& L, const SplitExchange& ex, int64_t seq, int layer,
                                            unsigned long long epoch) {
   half_t* slot = ex.kv + (seq * ex.layers + layer) * (2 * 64 * 128);
@@ -758,9 +772,11 @@ __device__ __forceinline__ void publish_kv(const Lds& L, const SplitExchange& ex
     *reinterpret_cast<half8_t*>(slot + 64 * 128 + 8 * e) =
         *reinterpret_cast<const half8_t*>(L.vt + (e / 8) * LD + 8 * (e % 8));
   }
-  __syncthreads();  // every thread's stores are done
+  __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (15 << 8) | (0 << 14));  // vmcnt(0): the L2 has the stores
+  __syncthreads();
   if (t == 0 && !ex.skip_publish)
-    __hip_atomic_store(ex.flags + seq * ex.layers + layer, epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(ex.flags + seq * ex.layers + layer, (epoch << 4) | xcd_id(), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ void fetch_kv(Lds& L, const SplitExchange& ex, int64_t seq, int layer,
@@ -769,20 +785,15 @@ __device__ __forceinline__ void fetch_kv(Lds& L, const SplitExchange& ex, int64_
   unsigned long long* flag = ex.flags + seq * ex.layers + layer;
   const int t = threadIdx.x;
   if (t == 0) {
-    // Poll with relaxed loads and acquire once after the loop: an acquiring
-    // load invalidates this XCD's L2 on every poll, evicting the weights the
-    // other workgroups there are reading.
-    int spins = 0;
-    while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != epoch) {
-      if (spins >= ex.spin_limit) {
-        atomicAdd(&ex.hdr->errors, 1);
-        L.poison = 1;
-        break;
-      }
+    unsigned long long v = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int spins = 0; (v >> 4) != epoch && spins < ex.spin_limit; ++spins) {
       __builtin_amdgcn_s_sleep(1);
-      ++spins;
+      v = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    if ((v >> 4) != epoch || (unsigned)(v & 15u) != xcd_id()) {  // timed out, or published on another XCD
+      atomicAdd(&ex.hdr->errors, 1);
+      L.poison = 1;
+    }
   }
   __syncthreads();
 #pragma unroll

@@ -306,14 +306,16 @@ int xb_fused_forward_d128(const float* x, float* y, const void* wpack,
  *     XB_ERR_WORKSPACE.  Its layout depends only on `layers`, so a workspace
  *     sized for a larger batch serves a smaller one (the size for the
  *     largest split batch serves every batch).  Its first 4 bytes (int32)
- *     count hand-offs that timed out (0 when every call was correct); bytes
+ *     count hand-offs that failed (0 when every call was correct); bytes
  *     8..15 (uint64) count completed split launches.
  *   spin_limit: sleeps (s_sleep 1 each) the second workgroup waits for a
  *     layer's K/V before it gives up; XB_SPLIT_SPINS_DEFAULT for the
  *     library's bound.  The two workgroups of a sequence run on one XCD with
  *     the first dispatched first, and the first never waits, so a wait only
- *     runs out when something else is broken.  A wait that runs out adds 1
- *     to the timeout counter and makes that workgroup's output rows NaN (the
+ *     runs out when something else is broken.  The K/V pass through that
+ *     XCD's L2 alone; the second workgroup checks that the first ran on its
+ *     XCD.  A wait that runs out, or a hand-off from another XCD, adds 1 to
+ *     the failure counter and makes that workgroup's output rows NaN (the
  *     kernel still completes), so a failed hand-off can never pass for a
  *     result.
  *   fault_flags: 0, or XB_SPLIT_FAULT_NO_PUBLISH to exercise that path.
