@@ -37,6 +37,7 @@ XB_MASK_SUM = 2
 XB_MASK_OUTPUT = 4
 XB_SPLIT_SPINS_DEFAULT = -1
 XB_SPLIT_FAULT_NO_PUBLISH = 1
+XB_SPLIT_FAULT_FOREIGN_XCD = 2
 XB_DECODE_SCRATCH_BYTES = 32 << 20
 XB_VARIANT_AUTO = -1
 XB_OP_LINEAR = 0

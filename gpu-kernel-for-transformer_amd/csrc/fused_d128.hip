@@ -742,6 +742,7 @@ struct SplitExchange {
   int layers;
   int spin_limit;                  // sleeps before a wait gives up
   int skip_publish;                // fault injection: part 0 never raises its flags
+  unsigned foreign_xcd;            // fault injection: 8 = part 0 signals with an id no XCD has (8..15)
 };
 
 __device__ __forceinline__ unsigned long long split_epoch(const SplitExchange& ex) {
@@ -775,8 +776,8 @@ __device__ __forceinline__ void publish_kv(const Lds& L, const SplitExchange& ex
   __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (15 << 8) | (0 << 14));  // vmcnt(0): the L2 has the stores
   __syncthreads();
   if (t == 0 && !ex.skip_publish)
-    __hip_atomic_store(ex.flags + seq * ex.layers + layer, (epoch << 4) | xcd_id(), __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(ex.flags + seq * ex.layers + layer, (epoch << 4) | (xcd_id() ^ ex.foreign_xcd),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ void fetch_kv(Lds& L, const SplitExchange& ex, int64_t seq, int layer,
@@ -1097,7 +1098,7 @@ __global__ __launch_bounds__(64 * NW, 1) void fused_stack8x2_kernel(
   }
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int pair = wave % 4;  // waves w and w + 4 (the two halves of blocks pair, 7 - pair) share a SIMD
-  const SplitExchange none{nullptr, nullptr, nullptr, 0, 0, 0};
+  const SplitExchange none{nullptr, nullptr, nullptr, 0, 0, 0, 0u};
   if (wave < 4)
     stack8x2_body<HD, 0, MASK, 2, false>(lds, x, y, wpack, ppack, S, layers, affine_mask, wave, pair, blockIdx.x, 0, none, 0);
   else
@@ -1202,7 +1203,8 @@ static hipError_t launch(const float* x, float* y, const half_t* w, const float*
                                    reinterpret_cast<unsigned long long*>(ws + kSplitHeaderBytes),
                                    reinterpret_cast<w8x2::SplitHeader*>(ws), layers,
                                    spin_limit < 0 ? kSplitDefaultSpins : spin_limit,
-                                   (fault_flags & XB_SPLIT_FAULT_NO_PUBLISH) ? 1 : 0};
+                                   (fault_flags & XB_SPLIT_FAULT_NO_PUBLISH) ? 1 : 0,
+                                   (fault_flags & XB_SPLIT_FAULT_FOREIGN_XCD) ? 8u : 0u};
       const int rounded = (int)((batch + 7) / 8 * 8);  // both parts of a sequence on one XCD
       const dim3 grid((unsigned)(2 * rounded)), block(64 * w8x2::NW);
       if (token_valid != nullptr)
@@ -1259,7 +1261,7 @@ static int fused_forward(const float* x, float* y, const void* wpack, const floa
   if (hd != 8 && hd != 16 && hd != 32 && hd != 64 && hd != 128) return XB_ERR_UNSUPPORTED_SHAPE;
   if (hd == 128 && (token_valid != nullptr || !causal)) return XB_ERR_UNSUPPORTED_SHAPE;  // eight-wave kernel: causal only
   if (ffn_dim != 128) return XB_ERR_UNSUPPORTED_SHAPE;
-  if (fault_flags & ~XB_SPLIT_FAULT_NO_PUBLISH) return XB_ERR_BAD_EPILOGUE;
+  if (fault_flags & ~(XB_SPLIT_FAULT_NO_PUBLISH | XB_SPLIT_FAULT_FOREIGN_XCD)) return XB_ERR_BAD_EPILOGUE;
   if (layers > 31) affine_mask = -1;  // bits beyond the mask: always affine
   if (batch == 0) return XB_OK;
   if (!x || !y || !wpack || !ppack) return XB_ERR_NULL_POINTER;

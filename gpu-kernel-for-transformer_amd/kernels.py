@@ -451,11 +451,13 @@ def fused_forward_d128(
     non-causal semantics of `attention` (padded rows come out zero).
     split=True lets a small causal batch run two workgroups per sequence
     (xb_fused_forward_d128_ws) with a workspace from `fused_split_workspace`;
-    the results are the same bit for bit.  A hand-off that timed out turns
-    the rows of the waiting workgroup into NaN and counts in the workspace;
-    strict=True also synchronises after the call and raises RuntimeError if
-    the count grew.  spin_limit / fault_flags are passed through (tests force
-    the time-out path with spin_limit=0, fault_flags=XB_SPLIT_FAULT_NO_PUBLISH).
+    the results are the same bit for bit.  A hand-off that failed (its wait
+    timed out, or it came from another XCD) turns the rows of the waiting
+    workgroup into NaN and counts in the workspace; strict=True also
+    synchronises after the call and raises RuntimeError if the count grew.
+    spin_limit / fault_flags are passed through (tests force the failure
+    paths with spin_limit=0 and fault_flags=XB_SPLIT_FAULT_NO_PUBLISH, or
+    with XB_SPLIT_FAULT_FOREIGN_XCD).
     """
     _require_device(x, "fused_forward_d128")
     if x.ndim != 3 or x.shape[-1] != 128 or x.dtype != torch.float32 or not x.is_contiguous():
@@ -478,8 +480,8 @@ def fused_forward_d128(
     if strict and ws is not None:
         grown = _split_timeouts_of(ws) - before
         if grown:
-            raise RuntimeError(f"fused_forward_d128: {grown} split-form K/V hand-off(s) timed out; "
-                               "the affected rows are NaN")
+            raise RuntimeError(f"fused_forward_d128: {grown} split-form K/V hand-off(s) failed (timed out, "
+                               "or published from another XCD); the affected rows are NaN")
     return out
 
 

@@ -285,6 +285,9 @@ int xb_fused_forward_d128(const float* x, float* y, const void* wpack,
 #define XB_SPLIT_FAULT_NO_PUBLISH 1    /* test only: the first workgroup of each
                                           sequence never signals its K/V, so every
                                           wait of the second runs out             */
+#define XB_SPLIT_FAULT_FOREIGN_XCD 2   /* test only: the first workgroup signals
+                                          with an XCD id no XCD has, so every
+                                          hand-off fails the second's XCD check   */
 
 /*
  * xb_fused_forward_d128 with a caller workspace that lets small batches use
@@ -318,7 +321,8 @@ int xb_fused_forward_d128(const float* x, float* y, const void* wpack,
  *     the failure counter and makes that workgroup's output rows NaN (the
  *     kernel still completes), so a failed hand-off can never pass for a
  *     result.
- *   fault_flags: 0, or XB_SPLIT_FAULT_NO_PUBLISH to exercise that path.
+ *   fault_flags: 0, or XB_SPLIT_FAULT_NO_PUBLISH / XB_SPLIT_FAULT_FOREIGN_XCD
+ *     to exercise those paths.
  * Replaces the same reference path as xb_fused_forward_d128.
  */
 int64_t xb_fused_forward_d128_workspace_bytes(int64_t batch, int32_t seq_len,

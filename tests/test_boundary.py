@@ -231,7 +231,7 @@ def test_argument_errors_need_no_gpu(capi):
     ws_args = (16, 16, 16, 16, 64, 128, 4, 128, 4, -1, None, 1)
     assert lib.xb_fused_forward_d128_ws(*ws_args, 16, need - 1, -1, 0, None) == -7
     assert lib.xb_fused_forward_d128_ws(*ws_args, 24, need, -1, 0, None) == -5
-    assert lib.xb_fused_forward_d128_ws(*ws_args, 16, need, -1, 2, None) == -6    # unknown fault flag
+    assert lib.xb_fused_forward_d128_ws(*ws_args, 16, need, -1, 4, None) == -6    # unknown fault flag
     assert lib.xb_fused_forward_d128_ws(16, 16, 16, 16, 64, 129, 4, 128, 4, -1, None, 1, 16, 1 << 30, -1, 0, None) == -4
     assert lib.xb_fused_forward_d128_ws(16, 16, 16, 16, 0, 128, 4, 128, 4, -1, None, 1, None, 0, -1, 0, None) == 0
     # No-allocation decode: a call whose partials exceed the static scratch is refused before any launch

@@ -548,16 +548,21 @@ def test_fused_split_graph_replay_and_smaller_batch(pkg, cuda):
         assert kernels.fused_split_timeouts(cuda) == timeouts and pool.timeouts() == 0
 
 
+@pytest.mark.parametrize("fault", ["no_publish", "foreign_xcd"])
 @pytest.mark.parametrize("geom", [(5, 128, 128, 4, 128, 2), (16, 100, 128, 16, 128, 3)])
-def test_fused_split_timeout_poisons_rows(pkg, cuda, geom):
-    """Force every hand-off to time out from the host (the first workgroup of
-    each sequence never signals, and the wait gives up at once): the waiting
-    workgroups' rows come out NaN, the other rows are the one-workgroup
-    kernel's, each wait is counted, every kernel still completes, and the next
-    normal call on the same workspace is exact again (no flag left behind can
-    satisfy it).  Strict mode turns the time-outs into a RuntimeError."""
+def test_fused_split_timeout_poisons_rows(pkg, cuda, geom, fault):
+    """Force every hand-off to fail from the host: either the first workgroup
+    of each sequence never signals and the wait gives up at once, or it
+    signals with an XCD id no XCD has (a hand-off that did not go through the
+    waiting workgroup's own L2).  The waiting workgroups' rows come out NaN,
+    the other rows are the one-workgroup kernel's, each hand-off is counted,
+    every kernel still completes, and the next normal call on the same
+    workspace is exact again (no flag left behind can satisfy it).  Strict
+    mode turns the failures into a RuntimeError."""
     kernels = __import__(pkg.__name__ + ".kernels", fromlist=["fused_forward_d128"])
     capi = __import__(pkg.__name__ + "._capi", fromlist=["XB_SPLIT_FAULT_NO_PUBLISH"])
+    forced = (dict(spin_limit=0, fault_flags=capi.XB_SPLIT_FAULT_NO_PUBLISH) if fault == "no_publish"
+              else dict(fault_flags=capi.XB_SPLIT_FAULT_FOREIGN_XCD))
     config = pkg.TransformerConfig(*geom, True)
     _, optimized = _models(pkg, config, cuda)
     b, s, layers = geom[0], geom[1], geom[5]
@@ -567,15 +572,13 @@ def test_fused_split_timeout_poisons_rows(pkg, cuda, geom):
     with torch.inference_mode():
         one = kernels.fused_forward_d128(xg, wpack, ppack, split=False, **args)
         before = kernels.fused_split_timeouts(cuda)
-        bad = kernels.fused_forward_d128(xg, wpack, ppack, spin_limit=0,
-                                         fault_flags=capi.XB_SPLIT_FAULT_NO_PUBLISH, **args)
+        bad = kernels.fused_forward_d128(xg, wpack, ppack, **forced, **args)
         torch.cuda.synchronize()
         assert kernels.fused_split_timeouts(cuda) - before == b * layers
         assert bool(torch.isnan(bad[:, 64:]).all()), "rows of the waiting workgroups must be NaN"
         assert torch.equal(bad[:, :64], one[:, :64]), "rows of the first workgroups are unaffected"
         good = kernels.fused_forward_d128(xg, wpack, ppack, strict=True, **args)
         assert torch.equal(good, one), "a call after the time-outs is exact"
-        with pytest.raises(RuntimeError, match="timed out"):
-            kernels.fused_forward_d128(xg, wpack, ppack, strict=True, spin_limit=0,
-                                       fault_flags=capi.XB_SPLIT_FAULT_NO_PUBLISH, **args)
+        with pytest.raises(RuntimeError, match="hand-off"):
+            kernels.fused_forward_d128(xg, wpack, ppack, strict=True, **forced, **args)
         assert torch.equal(kernels.fused_forward_d128(xg, wpack, ppack, strict=True, **args), one)
