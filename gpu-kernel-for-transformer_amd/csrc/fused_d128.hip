@@ -1167,16 +1167,15 @@ __global__ void pack_fragments_kernel(const float* __restrict__ w, half_t* __res
 }
 
 // The split form (two workgroups per sequence) needs causal attention and
-// tokens in both halves.  Its time grows with the batch even below 256
-// workgroups, the faster the fewer heads (measured at S = 128, 4 layers, in
-// us, one workgroup / split: head_dim 32 at B = 64 47.1 / 41.8, B = 80
-// 48.0 / 46.0, B = 96 48.1 / 49.5; head_dim 16 at B = 96 57.6 / 55.8, B = 112
-// 58.0 / 58.9; head_dim 8 at B = 112 76.7 / 73.0, B = 128 76.8 / 75.9), so it
-// stops at 80 sequences, 96 at head_dim 16 and 128 at head_dim 8.
-constexpr int64_t kSplitMaxBatch = 128;  // the largest of those limits (sets the workspace layout)
-static int64_t split_limit(int hd) { return hd <= 8 ? 128 : hd <= 16 ? 96 : 80; }
+// tokens in both halves.  Its time grows with the batch, but up to 128
+// sequences (256 workgroups, one per CU) it stays ahead of one workgroup per
+// sequence at every head_dim (S = 128, 4 layers, in us, one workgroup /
+// split: head_dim 64 at B = 64 45.7 / 38.7, B = 128 46.5 / 44.9; head_dim 32
+// 47.0 / 39.9 and 47.8 / 45.9; head_dim 16 55.4 / 43.7 and 56.1 / 49.8;
+// head_dim 8 73.6 / 58.5 and 74.3 / 64.8).
+constexpr int64_t kSplitMaxBatch = 128;  // the largest split batch (sets the workspace layout)
 static bool use_split(int64_t batch, int S, int hd, int causal) {
-  return hd <= 64 && causal && S > 64 && batch <= split_limit(hd);
+  return hd <= 64 && causal && S > 64 && batch <= kSplitMaxBatch;
 }
 // Workspace layout, the same for every batch of a layer count (so a workspace
 // made for the largest split batch serves all of them): a 256-byte header

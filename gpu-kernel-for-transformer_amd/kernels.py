@@ -485,7 +485,7 @@ def fused_forward_d128(
     return out
 
 
-_SPLIT_MAX_BATCHES = (128, 96, 80)  # the largest split batch at head_dim 8, 16, and above
+_SPLIT_MAX_BATCH = 128  # the largest batch the library splits (its workspace serves every smaller one)
 _SPLIT_WORKSPACES: dict = {}        # eager calls: (device, stream, layers) -> workspace
 _SPLIT_RETIRED: list = []
 _PRIVATE_POOLS: list = []           # stack of active SplitWorkspacePool scopes
@@ -519,8 +519,8 @@ class SplitWorkspacePool:
 
 def _new_split_workspace(device: torch.device, seq_len: int, num_heads: int, num_layers: int, causal: bool,
                          need: int) -> torch.Tensor:
-    size = max(int(lib().xb_fused_forward_d128_workspace_bytes(
-        b, int(seq_len), int(num_heads), int(num_layers), int(bool(causal)))) for b in _SPLIT_MAX_BATCHES)
+    size = int(lib().xb_fused_forward_d128_workspace_bytes(
+        _SPLIT_MAX_BATCH, int(seq_len), int(num_heads), int(num_layers), int(bool(causal))))
     return torch.zeros(max(size, need), device=device, dtype=torch.uint8)
 
 
@@ -563,7 +563,7 @@ def fused_split_workspace(device, batch: int, seq_len: int, num_heads: int, num_
     if ws is None:
         ws = _new_split_workspace(torch.device("cuda", index), seq_len, num_heads, num_layers, causal, need)
         _SPLIT_WORKSPACES[key] = ws
-    if ws.numel() < need:  # only if the library splits larger batches than _SPLIT_MAX_BATCHES
+    if ws.numel() < need:  # only if the library splits larger batches than _SPLIT_MAX_BATCH
         _SPLIT_RETIRED.append(ws)  # a graph captured before may still use it: never freed
         ws = torch.zeros(need, device=device, dtype=torch.uint8)
         _SPLIT_WORKSPACES[key] = ws

@@ -293,9 +293,8 @@ int xb_fused_forward_d128(const float* x, float* y, const void* wpack,
  * xb_fused_forward_d128 with a caller workspace that lets small batches use
  * two workgroups per sequence (tokens 0..63 and 64..127; the first hands each
  * layer's K and V of its tokens to the second through the workspace), which
- * doubles the CUs a small batch occupies (at most 80 sequences; 96 at
- * head_dim 16, 128 at head_dim 8).  Same results, bit for bit, as
- * xb_fused_forward_d128.
+ * doubles the CUs a small batch occupies (at most 128 sequences).  Same
+ * results, bit for bit, as xb_fused_forward_d128.
  *   xb_fused_forward_d128_workspace_bytes: bytes the split needs (0 = this
  *     shape runs one workgroup per sequence: head_dim above 64, causal = 0,
  *     seq_len <= 64 or a batch above those limits).

@@ -49,8 +49,8 @@ def test_shape_plan(pkg, capi):
     assert plan.describe().startswith("official-6: ffn=")
     assert plan.fused and plan.fused_variant == capi.XB_FUSED_PAIRS and plan.batch_chunk_size == 0
     assert "fused_stack_1wg_8wave_pairs" in plan.describe()
-    # small causal batches split each sequence over two workgroups
-    for shape_id in (1, 11):
+    # small causal batches (up to 128 sequences) split each sequence over two workgroups
+    for shape_id in (1, 5, 11):
         assert pkg.resolve_shape_execution_plan(shapes[shape_id]).fused_variant == capi.XB_FUSED_SPLIT
     # D=1024: per-op kernels; the QKV GEMM's tile is the cost model's (256 x 192 for N = 3072)
     cfg3 = pkg.resolve_shape_execution_plan(shapes[8])
@@ -219,11 +219,9 @@ def test_argument_errors_need_no_gpu(capi):
     head = lambda layers: (256 + 8 * 128 * layers + 255) // 256 * 256
     assert lib.xb_fused_forward_d128_workspace_bytes(64, 128, 4, 4, 1) == head(4) + 64 * 4 * slot
     assert lib.xb_fused_forward_d128_workspace_bytes(80, 65, 4, 2, 1) == head(2) + 80 * 2 * slot
-    assert lib.xb_fused_forward_d128_workspace_bytes(81, 128, 4, 4, 1) == 0    # head_dim 32: no gain from here on
-    assert lib.xb_fused_forward_d128_workspace_bytes(96, 128, 8, 4, 1) == head(4) + 96 * 4 * slot   # head_dim 16
-    assert lib.xb_fused_forward_d128_workspace_bytes(97, 128, 8, 4, 1) == 0
-    assert lib.xb_fused_forward_d128_workspace_bytes(128, 128, 16, 4, 1) == head(4) + 128 * 4 * slot  # head_dim 8
-    assert lib.xb_fused_forward_d128_workspace_bytes(129, 128, 16, 4, 1) == 0
+    for heads in (2, 4, 8, 16):  # up to 128 sequences (one workgroup per CU) at every head_dim <= 64
+        assert lib.xb_fused_forward_d128_workspace_bytes(128, 128, heads, 4, 1) == head(4) + 128 * 4 * slot
+        assert lib.xb_fused_forward_d128_workspace_bytes(129, 128, heads, 4, 1) == 0
     assert lib.xb_fused_forward_d128_workspace_bytes(64, 64, 4, 4, 1) == 0     # no second half
     assert lib.xb_fused_forward_d128_workspace_bytes(64, 128, 4, 4, 0) == 0    # non-causal
     assert lib.xb_fused_forward_d128_workspace_bytes(64, 128, 1, 4, 1) == 0    # head_dim 128
