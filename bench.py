@@ -28,6 +28,13 @@ Printed as ONE JSON line with, besides the driver's fields:
                   also times the reference's own shape-6 form (chunks of 1024
                   with a hipGraph per chunk shape, TTB:1740, :1826-1846)
   decode          KV-cached single-token steps at cfg5's geometry
+Timing: before the --warmup steps of every timed region, the step runs untimed
+until --settle seconds of wall time have passed (default 0.1).  An MI355X
+leaving idle needs about 30 ms of load before its clock settles: after 2 s
+idle, cfg2's first forwards take 2.6, 2.5, 2.3, 2.2 ms and reach 1.9 ms only
+from the 16th on, so 5 warm-up steps alone leave the ramp inside the timed
+steps.  Then --warmup untimed steps and exactly --steps timed ones, with a
+device synchronisation on both sides.
 A config whose device-memory estimate exceeds --memory-fraction of the GPU is
 skipped before anything is allocated, and an out-of-memory error skips it
 (the reference's SAFE_SKIP / SAFE_ABORT, streamed_shape14.py:197-222); for the
@@ -76,6 +83,8 @@ def parse_args(argv=None):
     p.add_argument("--decode-only", action="store_true",
                    help="run only the KV-cache decode measurement and print its JSON object (for rocprofv3)")
     p.add_argument("--rounds", type=int, default=1, help="headline: median ms over this many timed rounds of --steps")
+    p.add_argument("--settle", type=float, default=0.1,
+                   help="seconds of untimed steps before the warm-up steps of each timed region (GPU clock ramp)")
     p.add_argument("--batch", type=int, default=0,
                    help="run the headline with this batch instead of the shape's (the line then says so)")
     p.add_argument("--accuracy-trials", type=int, default=1,
@@ -85,8 +94,9 @@ def parse_args(argv=None):
     p.add_argument("--memory-fraction", type=float, default=0.9,
                    help="skip a config whose device-memory estimate exceeds this fraction of the GPU")
     args = p.parse_args(argv)
-    if args.steps <= 0 or args.warmup < 0 or args.rounds <= 0 or args.accuracy_trials <= 0 or args.batch < 0:
-        p.error("steps, rounds and accuracy trials must be positive; warmup and batch non-negative")
+    if (args.steps <= 0 or args.warmup < 0 or args.rounds <= 0 or args.accuracy_trials <= 0 or args.batch < 0
+            or args.settle < 0):
+        p.error("steps, rounds and accuracy trials must be positive; warmup, settle and batch non-negative")
     if not 0 < args.memory_fraction <= 1:
         p.error("--memory-fraction must be in (0, 1]")
     return args
@@ -376,7 +386,20 @@ def main(argv=None) -> int:
         g = torch.Generator(device=device).manual_seed(seed)
         return torch.randn(config.batch_size, config.seq_len, config.d_model, generator=g, device=device)
 
+    def settle(run):
+        """Untimed steps until args.settle seconds have passed (the clock ramp)."""
+        t0 = time.perf_counter()
+        batch = 1
+        while time.perf_counter() - t0 < args.settle:
+            t1 = time.perf_counter()
+            for _ in range(batch):
+                run()
+            torch.cuda.synchronize()
+            if time.perf_counter() - t1 < 0.01:
+                batch *= 2
+
     def time_steps(run, steps, warmup):
+        settle(run)
         for _ in range(warmup):
             run()
         torch.cuda.synchronize()
@@ -529,6 +552,7 @@ def main(argv=None) -> int:
         "n_gpus": 1,
         "steps": headline["steps"],
         "warmup": args.warmup,
+        "settle_s": args.settle,
         "rounds": args.rounds,
         "ms_per_step": headline["ms"],
         "higher_is_better": True,
