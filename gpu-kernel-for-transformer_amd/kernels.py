@@ -580,7 +580,7 @@ def split_launches_of(ws: torch.Tensor) -> int:
 
 
 def fused_split_timeouts(device=None) -> int:
-    """Hand-offs that timed out, summed over this process's eager split workspaces on `device`."""
+    """Failed hand-offs (timed out, or from another XCD), summed over this process's eager split workspaces on `device`."""
     total = 0
     for (index, _, _), ws in _SPLIT_WORKSPACES.items():
         if device is None or torch.device(device).index in (None, index):

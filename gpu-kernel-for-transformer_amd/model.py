@@ -227,9 +227,10 @@ class UserOptimizedTransformer(nn.Module):
         self._fused_stack_enabled = bool(enabled)
 
     def enable_strict_handoff_checks(self, enabled: bool = True) -> None:
-        """Synchronise after each split-form whole-stack launch and raise if a K/V hand-off timed out.
+        """Synchronise after each split-form whole-stack launch and raise if a K/V hand-off failed.
 
-        A timed-out hand-off already turns the affected output rows into NaN;
+        A failed hand-off (timed out, or published from another XCD) already
+        turns the affected output rows into NaN;
         this debug mode turns it into a RuntimeError at the call (one host
         sync per forward).
         """
