@@ -40,7 +40,7 @@ def _check(reference, candidate, label):
 
 
 @pytest.mark.parametrize("fused", [True, False])
-@pytest.mark.parametrize("shape_id", [1, 8, 11])
+@pytest.mark.parametrize("shape_id", [1, 5, 8, 11])
 def test_config_parity_two_trials(pkg, cuda, shape_id, fused):
     config = pkg.OFFICIAL_BENCHMARK_SHAPES[shape_id]
     baseline, optimized = _models(pkg, config, cuda)
@@ -460,7 +460,7 @@ def test_fused_stack_masks_and_non_causal(pkg, cuda, geom, causal):
     [((64, 128, 128, 4, 128, 4), False), ((80, 128, 128, 16, 128, 4), False), ((3, 100, 128, 8, 128, 2), True),
      ((5, 65, 128, 16, 128, 3), False), ((2, 128, 128, 2, 128, 2), True), ((4, 128, 128, 16, 128, 1), False),
      ((80, 127, 128, 4, 128, 33), False), ((1, 66, 128, 16, 128, 2), True), ((128, 128, 128, 16, 128, 2), False),
-     ((96, 100, 128, 8, 128, 2), True)],
+     ((96, 100, 128, 8, 128, 2), True), ((128, 128, 128, 4, 128, 2), False), ((112, 128, 128, 2, 128, 2), True)],
 )
 def test_fused_split_matches_one_workgroup(pkg, cuda, geom, masked):
     """Two workgroups per sequence (K/V of tokens 0..63 handed over through the
