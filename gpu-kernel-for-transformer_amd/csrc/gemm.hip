@@ -272,21 +272,29 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_kernel(
     stage = next;
   }
 
-  // Epilogue: lane owns C[m][n .. n+3] for each (i, j); bias (+ GELU) in FP32
-  // and one 8-byte store per fragment.
+  // Epilogue: bias (+ GELU) in FP32, the FP16 tile staged in LDS (free once
+  // every wave has read the last slab), then written out in 16-byte row
+  // chunks, a wave covering whole rows: lane-sized row pieces of 8 bytes
+  // scattered over 16 rows per store made the stores a fifth of the time.
+  // Chunk k of tile row r sits at chunk k ^ (r & SW) of its LDS row, which
+  // keeps both the 8-byte fragment writes and the 16-byte reads spread over
+  // the banks.
+  constexpr int CPR = BN / 8;                       // 16-byte chunks per tile row
+  constexpr int SW = CPR % 16 == 0 ? 15 : 7;
+  static_assert(BM * BN * 2 <= ST * SLAB, "the C tile fits in the slab stages");
+  slab_barrier();
+  half_t* cs = reinterpret_cast<half_t*>(smem);
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
-    const int n = n0 + wn + 16 * j + (lane / 16) * 4;
-    if (n >= N) continue;  // N % 8 == 0: n < N implies n + 3 < N
+    const int col = wn + 16 * j + (lane / 16) * 4;  // tile column of this lane's 4 values
     float b[4] = {0.f, 0.f, 0.f, 0.f};
-    if (bias != nullptr) {
+    if (bias != nullptr && n0 + col < N) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) b[e] = bias[n + e];
+      for (int e = 0; e < 4; ++e) b[e] = bias[n0 + col + e];
     }
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
-      const int m = m0 + wm + 16 * i + lane % 16;
-      if (m >= M) continue;
+      const int row = wm + 16 * i + lane % 16;
       half4_t h;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -294,8 +302,20 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_kernel(
         if constexpr (EPI == XB_EPI_BIAS_GELU) v = gelu_erf(v);
         h[e] = (half_t)v;
       }
-      *reinterpret_cast<half4_t*>(C + (int64_t)m * N + n) = h;
+      *reinterpret_cast<half4_t*>(cs + row * BN + 8 * ((col / 8) ^ (row & SW)) + (col & 7)) = h;
     }
+  }
+  slab_barrier();
+  constexpr int NT = 64 * NW;
+  static_assert((BM * CPR) % NT == 0, "whole rounds of 16-byte chunks");
+#pragma unroll
+  for (int id0 = 0; id0 < BM * CPR; id0 += NT) {
+    const int id = id0 + (int)threadIdx.x;
+    const int row = id / CPR, k = id % CPR;
+    const int gm = m0 + row, gn = n0 + 8 * k;
+    if (gm < M && gn < N)
+      *reinterpret_cast<half8_t*>(C + (int64_t)gm * N + gn) =
+          *reinterpret_cast<const half8_t*>(cs + row * BN + 8 * (k ^ (row & SW)));
   }
 }
 
