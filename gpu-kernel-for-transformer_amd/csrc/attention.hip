@@ -395,15 +395,20 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_kernel(const AttnArgs a)
     return;
   }
 
-  // Normalise and store: lane holds O^T[16hb + 4g + i][query r16]; every row of
-  // the all-ones block holds that query's probability sum.
-  half_t* obase = a.out + (int64_t)b * a.o_bstride + (int64_t)h * HD;
+  // Normalise: lane holds O^T[16hb + 4g + i][query r16]; every row of the
+  // all-ones block holds that query's probability sum.  The wave's rows go
+  // through LDS (its own rows of the freed K or V^T tiles) and leave as
+  // whole-row 16-byte chunks: stored straight from the accumulators, one
+  // store touched 16 rows with 8-byte pieces, and the stores took 30% of
+  // the head_dim-256 kernel's time.
+  static_assert(NBUF * BKEYS >= (NW - NW / 2) * QPW, "each wave's rows fit in the K or V^T tiles");
+  __syncthreads();  // every wave is done with the K/V tiles
+  half_t* const stg = wave < NW / 2 ? &k_lds[0][0] + wave * QPW * LDK : &v_lds[0][0] + (wave - NW / 2) * QPW * LDV;
+  const int rs = wave < NW / 2 ? LDK : LDV;
 #pragma unroll
   for (int qb = 0; qb < NQ; ++qb) {
     // A query that saw no key at all (every key masked) writes zeros.
     const float inv = lacc[qb][0] > 0.f ? __builtin_amdgcn_rcpf(lacc[qb][0]) : 0.f;
-    const int q = qw0 + 16 * qb + r16;
-    if (q >= S_q) continue;
 #pragma unroll
     for (int hb = 0; hb < HB; ++hb) {
       const int d = 16 * hb + 4 * g;
@@ -411,9 +416,20 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_kernel(const AttnArgs a)
         half4_t r;
 #pragma unroll
         for (int i = 0; i < 4; ++i) r[i] = (half_t)(o[hb][qb][i] * inv);
-        *reinterpret_cast<half4_t*>(obase + (int64_t)q * a.o_rstride + d) = r;
+        *reinterpret_cast<half4_t*>(stg + (16 * qb + r16) * rs + d) = r;
       }
     }
+  }
+  constexpr int CPR = HD / 8;  // 16-byte chunks per context row
+  half_t* obase = a.out + (int64_t)b * a.o_bstride + (int64_t)h * HD;
+#pragma unroll
+  for (int c0 = 0; c0 < QPW * CPR; c0 += kWave) {
+    const int c = c0 + lane;
+    const int row = c / CPR, k = c % CPR;
+    const int q = qw0 + row;
+    if (c < QPW * CPR && q < S_q)
+      *reinterpret_cast<half8_t*>(obase + (int64_t)q * a.o_rstride + 8 * k) =
+          *reinterpret_cast<const half8_t*>(stg + row * rs + 8 * k);
   }
 }
 
