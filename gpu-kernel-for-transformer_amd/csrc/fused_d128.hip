@@ -472,10 +472,21 @@ __device__ __forceinline__ void attend16(const half_t* k_lds, const half_t* vt_l
 #pragma unroll
     for (int j = 0; j < KSH; ++j) {
       qh[j] = qop[ks0 + j - OK * HALF];
-      if constexpr (HD < 32) {  // keep only this head's features of the shared k-step
-#pragma unroll
-        for (int m = 0; m < 8; ++m)
-          if ((32 * ks0 + 4 * g + (m & 3) + 16 * (m >> 2)) / HD != h) qh[j][m] = (half_t)0.f;
+      if constexpr (HD < 32) {
+        // Keep only this head's features of the shared k-step.  The lane's
+        // low four halves are features 4g..4g+3 of the k-step, its high four
+        // 16+4g..16+4g+3, so each group lies in one head: zero a whole
+        // 32-bit word pair instead of selecting half by half.
+        typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+        const int hrel = h % (32 / HD);  // head within the k-step
+        const bool keep_lo = HD == 16 ? hrel == 0 : (g >> 1) == hrel;
+        const bool keep_hi = HD == 16 ? hrel == 1 : (g >> 1) + 2 == hrel;
+        u32x4_t w = __builtin_bit_cast(u32x4_t, qh[j]);
+        w[0] = keep_lo ? w[0] : 0u;
+        w[1] = keep_lo ? w[1] : 0u;
+        w[2] = keep_hi ? w[2] : 0u;
+        w[3] = keep_hi ? w[3] : 0u;
+        qh[j] = __builtin_bit_cast(half8_t, w);
       }
     }
     float4_t sc[LKB + 1];
