@@ -779,7 +779,7 @@ __device__ __forceinline__ void publish_kv(const Lds& L, const SplitExchange& ex
   const int t = threadIdx.x;  // 512 threads, two 16-byte chunks of K and two of V^T each
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int e = 2 * t + i;  // 1024 chunks per region
+    const int e = t + 512 * i;  // 1024 chunks per region; one instruction writes 1 KB in a row
     *reinterpret_cast<half8_t*>(slot + 8 * e) = *reinterpret_cast<const half8_t*>(L.k + (e / 16) * LD + 8 * (e % 16));
     *reinterpret_cast<half8_t*>(slot + 64 * 128 + 8 * e) =
         *reinterpret_cast<const half8_t*>(L.vt + (e / 8) * LD + 8 * (e % 8));
@@ -810,7 +810,7 @@ __device__ __forceinline__ void fetch_kv(Lds& L, const SplitExchange& ex, int64_
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int e = 2 * t + i;
+    const int e = t + 512 * i;
     *reinterpret_cast<half8_t*>(L.k + (e / 16) * LD + 8 * (e % 16)) = *reinterpret_cast<const half8_t*>(slot + 8 * e);
     *reinterpret_cast<half8_t*>(L.vt + (e / 8) * LD + 8 * (e % 8)) =
         *reinterpret_cast<const half8_t*>(slot + 64 * 128 + 8 * e);
