@@ -450,7 +450,7 @@ struct Lds {
 // bytes kval (padding, and tokens past S).  MODE 2: no causal mask, key
 // validity only (every query block sees all eight key blocks).  In modes 1
 // and 2 a query may see no key at all: it then gets a zero context.
-template <int HD, int HALF, int QB, int MODE>
+template <int HD, int HALF, int QB, int MODE, bool DSTART = false>
 __device__ __forceinline__ void attend16(const half_t* k_lds, const half_t* vt_lds, const uint8_t* kval,
                                          const half8_t (&qop)[OK], half8_t (&cop)[KS], int g_in, int r16_in) {
   // Opaque copies: the lane-dependent head masks and addresses below are then
@@ -464,6 +464,17 @@ __device__ __forceinline__ void attend16(const half_t* k_lds, const half_t* vt_l
   constexpr int KSH = HD >= 32 ? HD / 32 : 1;
   constexpr int LKB = MODE == 2 ? 7 : QB;  // last key block
   constexpr int NKT = LKB / 2 + 1;          // 32-key steps of the PV product
+  // DSTART: the diagonal block's score accumulators start at -inf above the
+  // diagonal (key 4g + i after query r16), so the product leaves those
+  // scores at -inf and no head masks them again.  Otherwise each head masks
+  // its diagonal block after the product.  Both give the same values; the
+  // first is faster in the two-block (pair) form, the second in the split
+  // form.
+  float4_t dstart = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (MODE != 2 && DSTART) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dstart[i] = 4 * g + i > r16 ? -INFINITY : 0.f;
+  }
 #pragma unroll
   for (int hh = 0; hh < HH; ++hh) {
     const int h = HH * HALF + hh;
@@ -493,13 +504,13 @@ __device__ __forceinline__ void attend16(const half_t* k_lds, const half_t* vt_l
     float mx = -INFINITY;
 #pragma unroll
     for (int kb = 0; kb <= LKB; ++kb) {
-      float4_t acc = {0.f, 0.f, 0.f, 0.f};
+      float4_t acc = MODE != 2 && DSTART && kb == QB ? dstart : float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int j = 0; j < KSH; ++j) {
         const half8_t kf = *reinterpret_cast<const half8_t*>(k_lds + (16 * kb + r16) * LD + 32 * (ks0 + j) + 8 * g);
         acc = mfma16x16x32(kf, qh[j], acc);
       }
-      if (MODE != 2 && kb == QB) {  // -inf above the diagonal: key 4g + i vs query r16, formed here so nothing stays live
+      if (MODE != 2 && !DSTART && kb == QB) {  // -inf above the diagonal: key 4g + i vs query r16
 #pragma unroll
         for (int i = 0; i < 4; ++i)
           if (4 * g + i > r16) acc[i] = -INFINITY;
@@ -707,8 +718,8 @@ __device__ __forceinline__ void get_partner2(char* area, half8_t (&full)[NBT][KS
 template <int HD, int HALF, int P, int MASK>
 __device__ __forceinline__ void attend_pair(const Lds& L, const half8_t (&qop)[NB][OK], half8_t (&cop)[NB][KS], int g,
                                             int r16) {
-  split::attend16<HD, HALF, P, MASK>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16);
-  split::attend16<HD, HALF, 7 - P, MASK>(L.k, L.vt, L.kval, qop[1], cop[1], g, r16);
+  split::attend16<HD, HALF, P, MASK, true>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16);
+  split::attend16<HD, HALF, 7 - P, MASK, true>(L.k, L.vt, L.kval, qop[1], cop[1], g, r16);
 }
 
 // K/V exchange of the split form.  Per (sequence, layer) a 32 KB slot: K rows
