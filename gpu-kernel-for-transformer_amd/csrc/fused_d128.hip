@@ -545,8 +545,10 @@ __device__ __forceinline__ void attend16(const half_t* k_lds, const half_t* vt_l
       lacc = mfma16x16x32(ones, pf, lacc);
 #pragma unroll
       for (int hb = 0; hb < HDB; ++hb) {
-        const half_t* vr = vt_lds + (vrow0 + 16 * hb + r16) * LD + 32 * kt + 4 * g;
-        const half8_t vf = cat4(*reinterpret_cast<const half4_t*>(vr), *reinterpret_cast<const half4_t*>(vr + 16));
+        // V^T columns hold the keys of each 32-key step in the P operand's
+        // order (keys 32kt + 4g + i and 32kt + 16 + 4g + i at 32kt + 8g + i
+        // and + 4): one 16-byte read per fragment.
+        const half8_t vf = *reinterpret_cast<const half8_t*>(vt_lds + (vrow0 + 16 * hb + r16) * LD + 32 * kt + 8 * g);
         o[hb] = mfma16x16x32(vf, pf, o[hb]);
       }
     }
@@ -939,6 +941,8 @@ __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ 
         }
     }
     // ---- V (own features) -> V^T in LDS (after every wave has read area_b) --
+    // Columns in the attention's key order: token 16 tb + 4g + i at column
+    // 32 (tb / 2) + 8g + 4 (tb % 2) + i.
     {
       const char* st = begin_group(g0 + 1);
       float4_t a[NBT][OB];
@@ -953,7 +957,8 @@ __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ 
       for (int b = 0; b < NBT; ++b)
 #pragma unroll
         for (int j = 0; j < OB; ++j)
-          *reinterpret_cast<half4_t*>(vt_lds + (16 * (OB * half + j) + r16) * LD + 16 * tb[b] + 4 * g) =
+          *reinterpret_cast<half4_t*>(vt_lds + (16 * (OB * half + j) + r16) * LD + 32 * (tb[b] >> 1) + 8 * g +
+                                      4 * (tb[b] & 1)) =
               to_half4(a[b][j]);
     }
     // ---- Q (own heads), kept in registers --------------------------------
