@@ -22,12 +22,15 @@ from .config import (
 from .kernels import (
     attention,
     attention_kv_cache,
+    attention_vt,
     causal_attention,
     ffn_gelu,
     fused_residual_layer_norm,
     kv_cache_append,
     layer_norm,
     linear,
+    linear_qkv_vt,
+    vt_row_stride,
 )
 from .model import (
     SelfAttentionParameters,
@@ -50,6 +53,7 @@ __all__ = [
     "XBLOCK_LOAD_ERROR",
     "attention",
     "attention_kv_cache",
+    "attention_vt",
     "causal_attention",
     "ffn_gelu",
     "forward_bytes",
@@ -58,5 +62,7 @@ __all__ = [
     "kv_cache_append",
     "layer_norm",
     "linear",
+    "linear_qkv_vt",
     "resolve_shape_execution_plan",
+    "vt_row_stride",
 ]

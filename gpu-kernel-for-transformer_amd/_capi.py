@@ -57,6 +57,7 @@ XB_ATTN_W4_Q32 = 1
 XB_ATTN_W4_Q64 = 2
 XB_ATTN_W8_Q16 = 3
 XB_ATTN_PINGPONG = 4
+XB_ATTN_PINGPONG_VT = 5
 
 EXPORTED_SYMBOLS = (
     "xb_abi_version",
@@ -69,6 +70,9 @@ EXPORTED_SYMBOLS = (
     "xb_attention_causal",
     "xb_attention",
     "xb_attention_v",
+    "xb_vt_row_stride",
+    "xb_linear_qkv_vt",
+    "xb_attention_causal_vt",
     "xb_select_linear",
     "xb_select_attention",
     "xb_select_fused_d128",
@@ -105,6 +109,9 @@ _SIGNATURES = {
     "xb_attention": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i64, _i32, _i32, _f32, _i32, _vp]),
     "xb_linear_v": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, ctypes.c_int, ctypes.c_int, _vp]),
     "xb_attention_v": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i64, _i32, _i32, _f32, _i32, ctypes.c_int, _vp]),
+    "xb_vt_row_stride": (_i64, [_i64]),
+    "xb_linear_qkv_vt": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i32, _i32, _i32, ctypes.c_int, _vp]),
+    "xb_attention_causal_vt": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i64, _i32, _i32, _f32, _vp]),
     "xb_select_linear": (ctypes.c_int, [_i64, _i32, _i32, ctypes.c_int]),
     "xb_select_attention": (ctypes.c_int, [_i32, _i64, _i32, _i32, _i32]),
     "xb_select_fused_d128": (ctypes.c_int, [_i64, _i32, _i32, _i32, _i32, _i32]),

@@ -169,13 +169,16 @@ def resolve_shape_execution_plan(
     seq_len: Optional[int] = None,
     masked: bool = False,
     fused_allowed: bool = True,
+    transposed_v_allowed: bool = True,
 ) -> ShapeExecutionPlan:
     """The gfx950 plan for a forward of [batch, seq_len] (default: the config's own shape).
 
     masked: a padding mask with at least one False (the key-masked kernel
     forms).  fused_allowed: the caller's whole-stack
     conditions beyond the shape (the toggle, LayerNorm eps 1e-5 with affine
-    parameters).  The kernel choices are the library's (xb_select_*); only a
+    parameters).  transposed_v_allowed: the ping-pong attention may take V
+    transposed from the QKV GEMM (xb_linear_qkv_vt / xb_attention_causal_vt;
+    not for KV-cached steps, which attend through the cache).  The kernel choices are the library's (xb_select_*); only a
     batch whose working set exceeds CHUNK_BUDGET_FRACTION of HBM is chunked.
     Without the library the plan stays "unresolved" (the forward then raises).
     """
@@ -214,6 +217,15 @@ def resolve_shape_execution_plan(
     if missing:
         return ShapeExecutionPlan(official_shape_id=shape_id, batch=b, seq_len=s, masked=masked, batch_chunk_size=chunk,
                                   forward_strategy="unsupported (" + "; ".join(missing) + ")")
+    # The long-sequence (ping-pong) attention reads V transposed by the QKV
+    # GEMM when the shape allows it: causal, 32 | S, and a QKV tile whose
+    # width divides D, so every tile is all Q/K or all V.
+    if (transposed_v_allowed and attn == _capi.XB_ATTN_PINGPONG and config.causal and s % 32 == 0
+            and d % 128 == 0 and d >= 256):
+        widths = {_capi.XB_LINEAR_DMA_256x256: 256, _capi.XB_LINEAR_DMA_128x256: 256, _capi.XB_LINEAR_DMA_128x128: 128}
+        if d % widths.get(qkv, d + 1) != 0:
+            qkv = _capi.XB_LINEAR_DMA_256x256 if d % 256 == 0 else _capi.XB_LINEAR_DMA_128x128
+        attn = _capi.XB_ATTN_PINGPONG_VT
     lin = lambda v: _variant_name(lib, _capi.XB_OP_LINEAR, v)  # noqa: E731
     return ShapeExecutionPlan(
         official_shape_id=shape_id, batch=b, seq_len=s, masked=masked, batch_chunk_size=chunk,

@@ -80,6 +80,11 @@ struct AttnArgs {
   int q_rstride, k_rstride, o_rstride;
   int H, S_q, S_k, q_offset, q_tiles, n_splits, split_keys;
   float scale_log2;
+  // Ping-pong kernel only: V transposed per head by the QKV GEMM,
+  // vt[b][h][d][p] (rows of vt_row elements, key order inside each 32-key
+  // group as that GEMM writes it), used instead of v when not NULL.
+  const half_t* vt;
+  int64_t vt_row;
 };
 
 typedef short short4_t __attribute__((ext_vector_type(4)));
@@ -464,7 +469,7 @@ __device__ __forceinline__ void dma16_untracked(const void* src_lane, void* lds_
 // c ^ (r & 7), applied on the global side, which keeps the K fragment reads
 // and the transposing V reads free of bank conflicts.  Same arithmetic as
 // attn_kernel (offset in the score accumulator, lazy rescale, MFMA row sums).
-template <int HD, bool CAUSAL>
+template <int HD, bool CAUSAL, bool VT = false>
 __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
   constexpr int NQ = 4, NW = 8;
   using C = AttnCfg<HD, NQ, NW>;
@@ -492,6 +497,8 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
   const int64_t q_rstride = a.q_rstride, k_rstride = a.k_rstride;
   const half_t* kbase = a.k + (int64_t)b * a.k_bstride + (int64_t)h * a.k_hstride;
   const half_t* vbase = a.v + (int64_t)b * a.k_bstride + (int64_t)h * a.k_hstride;
+  // VT: row d of head (b, h) of the transposed V; tile t is its 128 bytes from key 64t.
+  const half_t* vtbase = VT ? a.vt + ((int64_t)b * a.H + h) * HD * a.vt_row : nullptr;
   const float scale_log2 = a.scale_log2;
 
   const int tid = threadIdx.x, lane = tid % kWave;
@@ -540,7 +547,10 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
     const int64_t off = (int64_t)min(t * BKEYS + ld_row, S_k - 1) * k_rstride + 8 * ld_chunk;
     const int buf = t & (NBUF - 1);
     dma16_untracked(kbase + off, &k_lds[buf][8 * wave * ROW]);
-    dma16_untracked(vbase + off, &v_lds[buf][8 * wave * ROW]);
+    if constexpr (VT)  // rows are head dims here; keys past S_k are the GEMM's zeros
+      dma16_untracked(vtbase + (int64_t)ld_row * a.vt_row + t * BKEYS + 8 * ld_chunk, &v_lds[buf][8 * wave * ROW]);
+    else
+      dma16_untracked(vbase + off, &v_lds[buf][8 * wave * ROW]);
   };
   // Barrier over LDS traffic only: the next tile's loads stay in flight ...
   auto half_step_barrier = [] {
@@ -624,13 +634,21 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(const AttnArgs a) {
     // ring of three; the row-sum products, which read no LDS, go first and
     // cover the first two reads.  The sched_barriers keep that order.
     half8_t vf[3];
+    // VT: the tile holds V^T (row = head dim, chunk 4kt + g = keys of the
+    // P operand's lane group g in step kt), one 16-byte read per fragment.
+    int tr = r16 * ROW, tg = g, ts = r16 & 7;
+    if constexpr (VT) asm volatile("" : "+v"(tr), "+v"(tg), "+v"(ts));
     auto read_v = [&](int step) {
       const int kt = step / HB, hb = step % HB;
-      const half_t* vrow = vt_lds + 32 * kt * ROW;
-      const int slot = 8 * (cb ^ (2 * hb));
-      const half4_t lo = lds_read_tr16(vrow + slot);
-      const half4_t hi = lds_read_tr16(vrow + 16 * ROW + slot);
-      vf[step % 3] = half8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      if constexpr (VT) {
+        vf[step % 3] = *reinterpret_cast<const half8_t*>(v_lds[t % NBUF] + 16 * hb * ROW + tr + 8 * ((4 * kt + tg) ^ ts));
+      } else {
+        const half_t* vrow = vt_lds + 32 * kt * ROW;
+        const int slot = 8 * (cb ^ (2 * hb));
+        const half4_t lo = lds_read_tr16(vrow + slot);
+        const half4_t hi = lds_read_tr16(vrow + 16 * ROW + slot);
+        vf[step % 3] = half8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      }
     };
     read_v(0);
     read_v(1);
@@ -840,6 +858,10 @@ static hipError_t launch_attn_pp(AttnArgs a, int B, int causal, hipStream_t s) {
   a.q_tiles = (a.S_q + BQ - 1) / BQ;
   const int64_t blocks = (int64_t)a.q_tiles * B * a.H;
   if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
+  if (a.vt != nullptr) {  // causal only (the caller checked)
+    hipLaunchKernelGGL((attn_pp_kernel<HD, true, true>), dim3((unsigned)blocks), dim3(512), 0, s, a);
+    return hipGetLastError();
+  }
   if (causal)
     hipLaunchKernelGGL((attn_pp_kernel<HD, true>), dim3((unsigned)blocks), dim3(512), 0, s, a);
   else
@@ -1025,6 +1047,34 @@ extern "C" int xb_attention_v(const void* qkv, void* out, const uint8_t* key_val
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int c = causal ? 1 : 0;
   return (int)by_head_dim(head_dim, [&](auto hd) { return run_attn<decltype(hd)::value>(variant, a, batch, c, s); });
+}
+
+extern "C" int xb_attention_causal_vt(const void* qkv, const void* vt, void* out, int32_t batch, int64_t seq_len,
+                                      int32_t heads, int32_t head_dim, float scale, void* stream) {
+  const int bad = check_attention(batch, seq_len, heads, head_dim);
+  if (bad) return bad;
+  if (head_dim != 64 || seq_len % 32 != 0) return XB_ERR_UNSUPPORTED_SHAPE;
+  if (batch == 0 || seq_len == 0) return XB_OK;
+  if (!qkv || !vt || !out) return XB_ERR_NULL_POINTER;
+  if (((uintptr_t)qkv | (uintptr_t)vt | (uintptr_t)out) & 15u) return XB_ERR_MISALIGNED;
+  const int S = (int)seq_len;
+  const int64_t D = (int64_t)heads * head_dim;
+  AttnArgs a = {};
+  a.q = static_cast<const half_t*>(qkv);
+  a.k = a.q + D;
+  a.v = nullptr;
+  a.vt = static_cast<const half_t*>(vt);
+  a.vt_row = (seq_len + 63) / 64 * 64;
+  a.out = static_cast<half_t*>(out);
+  a.q_bstride = a.k_bstride = (int64_t)S * 3 * D;
+  a.k_hstride = head_dim;
+  a.o_bstride = (int64_t)S * D;
+  a.q_rstride = a.k_rstride = (int)(3 * D);
+  a.o_rstride = (int)D;
+  a.H = heads;
+  a.S_q = a.S_k = S;
+  a.scale_log2 = scale * 1.44269504088896340736f;
+  return (int)launch_attn_pp<64>(a, batch, 1, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int xb_attention(const void* qkv, void* out, const uint8_t* key_valid, int32_t batch,

@@ -46,6 +46,7 @@ extern "C" const char* xb_variant_name(int op, int variant) {
         case XB_ATTN_W4_Q64: return "flash_4wave_256q";
         case XB_ATTN_W8_Q16: return "flash_8wave_128q";
         case XB_ATTN_PINGPONG: return "flash_pingpong_8wave_512q";
+        case XB_ATTN_PINGPONG_VT: return "flash_pingpong_vt_8wave_512q";
         default: return nullptr;
       }
     case XB_OP_FUSED_D128:

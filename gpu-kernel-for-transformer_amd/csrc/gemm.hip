@@ -185,11 +185,23 @@ __device__ __forceinline__ void slab_barrier() {
 
 __device__ __forceinline__ int row128_offset(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
 
-template <int BM, int BN, int WGM, int WGN, int EPI, int ST>
+// V of a packed QKV projection written transposed per head for the long-
+// sequence attention: vt[b][h][d][p] with rows of `row` = seq_len rounded up
+// to 64 elements, the positions p of each 32-token group in the attention's
+// key order (token 32t + 4g + i at 32t + 8g + i, token 32t + 16 + 4g + i at
+// 32t + 8g + 4 + i), so one 16-byte LDS read there is one operand fragment.
+// Positions seq_len .. row-1 hold zeros.  Columns from v_col0 on are V.
+struct VtOut {
+  half_t* vt;
+  int64_t row;
+  int seq_len, head_dim, heads, v_col0;
+};
+
+template <int BM, int BN, int WGM, int WGN, int EPI, int ST, bool VT = false>
 __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_kernel(
     const half_t* __restrict__ A, const half_t* __restrict__ W,
     const float* __restrict__ bias, half_t* __restrict__ C, int M, int N,
-    int K, int tiles_n) {
+    int K, int tiles_n, VtOut vo) {
   constexpr int NW = WGM * WGN;
   constexpr int WM = BM / WGM, WN = BN / WGN, FM = WM / 16, FN = WN / 16;
   constexpr int SLAB = (BM + BN) * 128;        // 64-wide K slab, 128-byte rows
@@ -283,6 +295,49 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_kernel(
   constexpr int SW = CPR % 16 == 0 ? 15 : 7;
   static_assert(BM * BN * 2 <= ST * SLAB, "the C tile fits in the slab stages");
   slab_barrier();
+  if constexpr (VT) {
+    if (n0 >= vo.v_col0) {  // a V tile (the host checked v_col0 % BN == 0, seq_len % 32 == 0)
+      static_assert(BM % 32 == 0, "whole 32-token groups per tile");
+      // Staged feature-major, [BN][BM], positions in key order, then written
+      // as whole 16-byte chunks of the transposed rows.
+      half_t* vs = reinterpret_cast<half_t*>(smem);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int col = wn + 16 * j + (lane / 16) * 4;
+        float b[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) b[e] = bias != nullptr ? bias[n0 + col + e] : 0.f;
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          const int r = wm + 16 * i + lane % 16;
+          const int p = (r & ~31) | (((r & 15) >> 2) << 3) | (((r >> 4) & 1) << 2) | (r & 3);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) vs[(col + e) * BM + p] = (half_t)(acc[i][j][e] + b[e]);
+        }
+      }
+      slab_barrier();
+      constexpr int NT = 64 * NW, CPF = BM / 8;  // 16-byte chunks per staged feature row
+      static_assert((BN * CPF) % NT == 0, "whole rounds of chunks");
+#pragma unroll
+      for (int id0 = 0; id0 < BN * CPF; id0 += NT) {
+        const int id = id0 + (int)threadIdx.x;
+        const int f = id / CPF, c = id % CPF;
+        const int m = m0 + 32 * (c / 4);  // first token of the chunk's 32-token group
+        if (m < M) {
+          const int bq = m / vo.seq_len, sq = m - bq * vo.seq_len;
+          const int n = n0 + f - vo.v_col0;
+          const int h = n / vo.head_dim, d = n - h * vo.head_dim;
+          half_t* dst = vo.vt + ((int64_t)(bq * vo.heads + h) * vo.head_dim + d) * vo.row + sq + 8 * (c % 4);
+          *reinterpret_cast<half8_t*>(dst) = *reinterpret_cast<const half8_t*>(vs + f * BM + 8 * c);
+          if (sq + 32 == vo.seq_len && c % 4 == 0) {  // the sequence's last group: zero the row's padding
+            for (int64_t z = vo.seq_len; z < vo.row; z += 8)
+              *reinterpret_cast<half8_t*>(dst - sq + z) = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+          }
+        }
+      }
+      return;
+    }
+  }
   half_t* cs = reinterpret_cast<half_t*>(smem);
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
@@ -319,13 +374,13 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_kernel(
   }
 }
 
-template <int BM, int BN, int WGM, int WGN, int EPI, int ST>
+template <int BM, int BN, int WGM, int WGN, int EPI, int ST, bool VT = false>
 static hipError_t launch_gemm_dma(const half_t* a, const half_t* w, const float* bias, half_t* c,
-                                  int64_t m, int n, int k, hipStream_t s) {
+                                  int64_t m, int n, int k, hipStream_t s, VtOut vo = {}) {
   const int64_t tm = (m + BM - 1) / BM, tn = (n + BN - 1) / BN;
   if (tm * tn > 0x7fffffffLL) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, WGM, WGN, EPI, ST>), dim3((unsigned)(tm * tn)),
-                     dim3(64 * WGM * WGN), 0, s, a, w, bias, c, (int)m, n, k, (int)tn);
+  hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, WGM, WGN, EPI, ST, VT>), dim3((unsigned)(tm * tn)),
+                     dim3(64 * WGM * WGN), 0, s, a, w, bias, c, (int)m, n, k, (int)tn, vo);
   return hipGetLastError();
 }
 
@@ -424,4 +479,46 @@ extern "C" int xb_linear_v(const void* a, const void* w, const float* bias, void
 extern "C" int xb_linear(const void* a, const void* w, const float* bias, void* c,
                          int64_t m, int32_t n, int32_t k, int epilogue, void* stream) {
   return xb_linear_v(a, w, bias, c, m, n, k, epilogue, XB_VARIANT_AUTO, stream);
+}
+
+extern "C" int64_t xb_vt_row_stride(int64_t seq_len) { return seq_len <= 0 ? 0 : (seq_len + 63) / 64 * 64; }
+
+extern "C" int xb_linear_qkv_vt(const void* a, const void* w, const float* bias, void* qkv, void* vt,
+                                int32_t batch, int64_t seq_len, int32_t heads, int32_t head_dim, int32_t k,
+                                int variant, void* stream) {
+  if (batch < 0 || seq_len < 0 || heads <= 0 || head_dim <= 0 || k <= 0) return XB_ERR_BAD_SIZE;
+  const int64_t m = (int64_t)batch * seq_len;
+  const int64_t d = (int64_t)heads * head_dim;
+  if (m > 0x7fffffffLL || 3 * d > 0x7fffffffLL) return XB_ERR_BAD_SIZE;
+  const int n = (int)(3 * d);
+  if (seq_len % 32 != 0 || head_dim % 8 != 0 || k % 64 != 0 || k < 256) return XB_ERR_UNSUPPORTED_SHAPE;
+  if (variant == XB_VARIANT_AUTO) {
+    variant = select_linear(m, n, k);
+    if (variant == XB_LINEAR_DMA_256x192 || d % 256 != 0) variant = d % 256 == 0 ? XB_LINEAR_DMA_256x256 : XB_LINEAR_DMA_128x128;
+  }
+  int bn = 0;
+  switch (variant) {
+    case XB_LINEAR_DMA_256x256: case XB_LINEAR_DMA_128x256: bn = 256; break;
+    case XB_LINEAR_DMA_128x128: bn = 128; break;
+    default: return XB_ERR_BAD_VARIANT;  // the V boundary must fall between DMA tiles
+  }
+  if (d % bn != 0) return XB_ERR_BAD_VARIANT;  // every tile is all Q/K or all V
+  if (m == 0) return XB_OK;
+  if (!a || !w || !qkv || !vt) return XB_ERR_NULL_POINTER;
+  if (((uintptr_t)a | (uintptr_t)w | (uintptr_t)qkv | (uintptr_t)vt) & 15u) return XB_ERR_MISALIGNED;
+  const VtOut vo{static_cast<half_t*>(vt), xb_vt_row_stride(seq_len), (int)seq_len, head_dim, heads, (int)(2 * d)};
+  const half_t* A = static_cast<const half_t*>(a);
+  const half_t* Wt = static_cast<const half_t*>(w);
+  half_t* Cc = static_cast<half_t*>(qkv);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  switch (variant) {
+    case XB_LINEAR_DMA_256x256:
+      e = launch_gemm_dma<256, 256, 4, 2, XB_EPI_BIAS, 2, true>(A, Wt, bias, Cc, m, n, k, s, vo); break;
+    case XB_LINEAR_DMA_128x256:
+      e = launch_gemm_dma<128, 256, 2, 4, XB_EPI_BIAS, 2, true>(A, Wt, bias, Cc, m, n, k, s, vo); break;
+    default:
+      e = launch_gemm_dma<128, 128, 2, 2, XB_EPI_BIAS, 2, true>(A, Wt, bias, Cc, m, n, k, s, vo); break;
+  }
+  return (int)e;
 }

@@ -311,6 +311,90 @@ def attention(
     return out
 
 
+def vt_row_stride(seq_len: int) -> int:
+    """Row length (elements) of the transposed-V buffer: seq_len rounded up to 64."""
+    return int(lib().xb_vt_row_stride(int(seq_len)))
+
+
+def linear_qkv_vt(
+    inputs: torch.Tensor,
+    weight: torch.Tensor,
+    bias: Optional[torch.Tensor],
+    num_heads: int,
+    out: Optional[torch.Tensor] = None,
+    vt: Optional[torch.Tensor] = None,
+    variant: int = _capi.XB_VARIANT_AUTO,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The packed QKV projection with V written transposed for `attention_vt`.
+
+    inputs: [B, S, K] float16; weight: [3D, K] float16; bias: [3D] float32 or
+    None.  Returns (qkv, vt): qkv [B, S, 3D] with the Q and K columns of
+    `linear(inputs, weight, bias)` (the V columns are left unwritten) and vt
+    [B, H, head_dim, vt_row_stride(S)] holding V per head dimension, each
+    32-token group in the attention's key order, zeros past S.  Needs S % 32
+    == 0, K % 64 == 0 and K >= 256; the long-sequence attention reads it
+    (head_dim 64).
+    """
+    _require_device(inputs, "linear_qkv_vt")
+    if inputs.ndim != 3 or weight.ndim != 2:
+        raise ValueError("inputs must be [B, S, K] and weight 2-D")
+    if inputs.dtype != torch.float16 or weight.dtype != torch.float16:
+        raise ValueError("linear_qkv_vt expects float16 inputs and weights")
+    if not inputs.is_contiguous() or not weight.is_contiguous():
+        raise ValueError("linear_qkv_vt expects contiguous inputs and weights")
+    if bias is not None and (bias.dtype != torch.float32 or bias.numel() != weight.shape[0]):
+        raise ValueError("bias must be float32 with one entry per output feature")
+    batch, seq_len, k = inputs.shape
+    n = weight.shape[0]
+    if weight.shape[1] != k or n % (3 * num_heads) != 0:
+        raise ValueError("weight must be [3 * num_heads * head_dim, K]")
+    head_dim = n // (3 * num_heads)
+    if out is None:
+        out = torch.empty((batch, seq_len, n), device=inputs.device, dtype=torch.float16)
+    if vt is None:
+        vt = torch.empty((batch, num_heads, head_dim, vt_row_stride(seq_len)), device=inputs.device,
+                         dtype=torch.float16)
+    check(
+        _launch(f"gemm_n{n}_k{k}_vt", lambda: lib().xb_linear_qkv_vt(
+            inputs.data_ptr(), weight.data_ptr(), _ptr(bias), out.data_ptr(), vt.data_ptr(), batch, seq_len,
+            num_heads, head_dim, k, int(variant), stream_handle(inputs.device),
+        )),
+        "xb_linear_qkv_vt",
+    )
+    return out, vt
+
+
+def attention_vt(
+    qkv: torch.Tensor,
+    vt: torch.Tensor,
+    num_heads: int,
+    scale: Optional[float] = None,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Causal attention over (qkv, vt) from `linear_qkv_vt`: the same values as
+    causal_attention over the full projection, bit for bit (head_dim 64)."""
+    _require_device(qkv, "attention_vt")
+    if qkv.ndim != 3 or qkv.shape[-1] % (3 * num_heads) != 0:
+        raise ValueError("qkv must be [B, S, 3 * num_heads * head_dim]")
+    batch, seq_len, width = qkv.shape
+    d_model = width // 3
+    head_dim = d_model // num_heads
+    if tuple(vt.shape) != (batch, num_heads, head_dim, vt_row_stride(seq_len)) or vt.dtype != torch.float16:
+        raise ValueError("vt must be the [B, H, head_dim, vt_row_stride(S)] float16 buffer of linear_qkv_vt")
+    if scale is None:
+        scale = head_dim ** -0.5
+    if out is None:
+        out = torch.empty((batch, seq_len, d_model), device=qkv.device, dtype=torch.float16)
+    check(
+        _launch(f"attention_hd{head_dim}_vt", lambda: lib().xb_attention_causal_vt(
+            qkv.data_ptr(), vt.data_ptr(), out.data_ptr(), batch, seq_len, num_heads, head_dim, float(scale),
+            stream_handle(qkv.device),
+        )),
+        "xb_attention_causal_vt",
+    )
+    return out
+
+
 def _check_kv_cache(qkv: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, num_heads: int) -> Tuple[int, int, int, int]:
     if qkv.ndim != 3 or qkv.shape[-1] % (3 * num_heads) != 0:
         raise ValueError("qkv must be [B, chunk, 3 * num_heads * head_dim]")

@@ -173,11 +173,12 @@ class UserOptimizedTransformer(nn.Module):
         eligibility (the enable_fused_stack toggle, LayerNorm eps and affine);
         per_op=True asks for the per-op sequence (KV-cached steps).
         """
-        key = (int(batch), int(seq_len), bool(padded), self._fused_stack_eligible() and not per_op)
+        key = (int(batch), int(seq_len), bool(padded), self._fused_stack_eligible() and not per_op, bool(per_op))
         plans = self.__dict__.setdefault("_plans", {})
         plan = plans.get(key)
         if plan is None:
-            plan = resolve_shape_execution_plan(self.config, batch, seq_len, masked=padded, fused_allowed=key[3])
+            plan = resolve_shape_execution_plan(self.config, batch, seq_len, masked=padded, fused_allowed=key[3],
+                                                transposed_v_allowed=not per_op)
             plans[key] = plan
         return plan
 
@@ -491,6 +492,13 @@ class UserOptimizedTransformer(nn.Module):
         f16 = torch.float16
         num_layers = len(self.layers)
 
+        # The long-sequence attention reading V transposed by the QKV GEMM
+        # (one buffer for all layers).
+        transposed_v = plan.attention_variant == _capi.XB_ATTN_PINGPONG_VT
+        vt = None
+        if transposed_v:
+            vt = torch.empty((batch, cfg.num_heads, cfg.head_dim, kernels.vt_row_stride(seq_len)), device=dev,
+                             dtype=torch.float16)
         first = self.layers[0].norm1
         norm = kernels.layer_norm(x, first.weight, first.bias, first.eps, f16, apply_affine=self._layer_norm_uses_affine(first))
         residual_in = x
@@ -499,8 +507,12 @@ class UserOptimizedTransformer(nn.Module):
             out = torch.empty_like(x)
         for index, layer in enumerate(self.layers):
             w = self._layer_weights(index)
-            qkv = kernels.linear(norm, w.qkv_w, w.qkv_b, variant=plan.qkv_variant)
-            context = attend(index, layer, qkv)
+            if transposed_v:
+                qkv, _ = kernels.linear_qkv_vt(norm, w.qkv_w, w.qkv_b, cfg.num_heads, vt=vt, variant=plan.qkv_variant)
+                context = kernels.attention_vt(qkv, vt, cfg.num_heads, scale=layer.attention.scale)
+            else:
+                qkv = kernels.linear(norm, w.qkv_w, w.qkv_b, variant=plan.qkv_variant)
+                context = attend(index, layer, qkv)
             update = kernels.linear(context, w.out_w, w.out_b, variant=plan.out_variant)
             residual_in, norm2 = kernels.fused_residual_layer_norm(
                 residual_in, update, layer.norm2.weight, layer.norm2.bias, layer.norm2.eps, f16,

@@ -78,6 +78,8 @@ const char* xb_strerror(int code);
 #define XB_ATTN_W4_Q64 2     /* head_dim <= 64                            */
 #define XB_ATTN_W8_Q16 3     /* head_dim 256                              */
 #define XB_ATTN_PINGPONG 4   /* head_dim 64, no key mask: 512 queries      */
+#define XB_ATTN_PINGPONG_VT 5 /* XB_ATTN_PINGPONG reading V transposed by xb_linear_qkv_vt:
+                                 runs through xb_attention_causal_vt only  */
 /* xb_fused_forward_d128[_ws]: which form runs (the split needs a workspace). */
 #define XB_FUSED_PAIRS 0     /* one workgroup per sequence, 8 waves x 2 token blocks (head_dim <= 64) */
 #define XB_FUSED_SPLIT 1     /* two workgroups per sequence (xb_fused_forward_d128_ws)                */
@@ -174,6 +176,36 @@ int xb_attention_v(const void* qkv, void* out, const uint8_t* key_valid,
                    int32_t batch, int64_t seq_len, int32_t heads,
                    int32_t head_dim, float scale, int32_t causal, int variant,
                    void* stream);
+
+/*
+ * The QKV projection and causal attention of long sequences with V handed
+ * over transposed.  No reference counterpart: together they replace the
+ * packed QKV F.linear and F.scaled_dot_product_attention(is_causal=True) of
+ * torch_transformer_benchmark.py:741-809 (as xb_linear + xb_attention_causal
+ * do) for head_dim 64 and seq_len % 32 == 0, the shapes that take the
+ * ping-pong attention kernel (long sequences, no key mask).
+ *
+ * xb_linear_qkv_vt: qkv[M, 3D] = a[M, K] . w[3D, K]^T + bias as xb_linear
+ * (M = batch * seq_len, D = heads * head_dim) for the Q and K columns only;
+ * V goes to vt, [batch, heads, head_dim, xb_vt_row_stride(seq_len)] FP16,
+ * each row holding one head dimension over the sequence with every 32-token
+ * group in the attention's key order (token 32t + 4g + i at position
+ * 32t + 8g + i, token 32t + 16 + 4g + i at 32t + 8g + 4 + i, g, i < 4) and
+ * zeros past seq_len.  qkv's V columns are left unwritten.  variant: a
+ * gemm_dma_kernel tile whose width divides D (XB_LINEAR_DMA_256x256,
+ * _128x256, _128x128) or XB_VARIANT_AUTO; K % 64 == 0 and K >= 256.
+ *
+ * xb_attention_causal_vt: out = xb_attention_causal(qkv) with V read from vt;
+ * bit for bit the same result.
+ */
+int64_t xb_vt_row_stride(int64_t seq_len);
+int xb_linear_qkv_vt(const void* a, const void* w, const float* bias,
+                     void* qkv, void* vt, int32_t batch, int64_t seq_len,
+                     int32_t heads, int32_t head_dim, int32_t k, int variant,
+                     void* stream);
+int xb_attention_causal_vt(const void* qkv, const void* vt, void* out,
+                           int32_t batch, int64_t seq_len, int32_t heads,
+                           int32_t head_dim, float scale, void* stream);
 
 /*
  * KV cache for incremental causal decoding (replaces _append_kv_cache and the

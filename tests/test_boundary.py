@@ -57,7 +57,13 @@ def test_shape_plan(pkg, capi):
     assert not cfg3.fused and cfg3.qkv_variant == 1 and "mfma_gemm_dma_256x192" in cfg3.projection_strategy
     assert cfg3.attention_strategy == "flash_8wave_128q"
     cfg5 = pkg.resolve_shape_execution_plan(shapes[14])
-    assert cfg5.attention_strategy == "flash_pingpong_8wave_512q" and cfg5.batch_chunk_size == 0
+    assert cfg5.attention_strategy == "flash_pingpong_vt_8wave_512q" and cfg5.batch_chunk_size == 0
+    assert cfg5.attention_variant == capi.XB_ATTN_PINGPONG_VT and cfg5.qkv_variant == capi.XB_LINEAR_DMA_256x256
+    # V transposed by the QKV GEMM needs 32 | S and is not used for KV-cached steps
+    odd = pkg.TransformerConfig(2, 100001, 1024, 16, 1024, 2, True)
+    assert pkg.resolve_shape_execution_plan(odd).attention_strategy == "flash_pingpong_8wave_512q"
+    assert pkg.resolve_shape_execution_plan(shapes[14], transposed_v_allowed=False).attention_variant == \
+        capi.XB_ATTN_PINGPONG
     # a padded mask takes the key-masked forms: no ping-pong kernel
     assert pkg.resolve_shape_execution_plan(shapes[14], masked=True).attention_strategy == "flash_4wave_256q"
     # the whole-stack kernel off (toggle or LayerNorm contract): per-op

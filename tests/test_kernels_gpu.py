@@ -193,6 +193,78 @@ def test_attention_long_hd64_ping_pong(pkg, cuda, b, s, h, causal):
     assert torch.equal(out, pkg.attention(qg, h, key_valid=ones, causal=causal))
 
 
+def _key_order(s):
+    """Position of each token of a row of the transposed V: inside every
+    32-token group, token 32t + 4g + i sits at 32t + 8g + i and token
+    32t + 16 + 4g + i at 32t + 8g + 4 + i (the attention's key order)."""
+    t = torch.arange(s)
+    r = t % 32
+    return t - r + 8 * ((r % 16) // 4) + 4 * (r // 16) + r % 4
+
+
+@pytest.mark.parametrize("b,s,h,k", [(2, 96, 4, 256), (3, 160, 8, 512), (1, 4160, 16, 1024)])
+def test_linear_qkv_vt_layout(pkg, cuda, b, s, h, k):
+    """The QKV GEMM with V written transposed: Q and K columns bitwise those of
+    xb_linear, vt[b, h, d, position(s)] bitwise V[b, s, h, d], zeros past S
+    (row stride S rounded up to 64), for every tile variant it accepts."""
+    capi = pkg._capi
+    hd, d = 64, h * 64
+    x = torch.randn(b, s, k, generator=_gen(s + k)).half().to(cuda)
+    w = (torch.randn(3 * d, k, generator=_gen(k)) / k ** 0.5).half().to(cuda)
+    bias = torch.randn(3 * d, generator=_gen(d)).to(cuda)
+    full = pkg.linear(x, w, bias)
+    v = full[..., 2 * d:].reshape(b, s, h, hd).permute(0, 2, 3, 1)  # [b, h, hd, s]
+    row = pkg.vt_row_stride(s)
+    assert row == (s + 63) // 64 * 64
+    pos = _key_order(s).to(cuda)
+    variants = [capi.XB_VARIANT_AUTO, capi.XB_LINEAR_DMA_256x256, capi.XB_LINEAR_DMA_128x256,
+                capi.XB_LINEAR_DMA_128x128]
+    for variant in variants:
+        if variant in (capi.XB_LINEAR_DMA_256x256, capi.XB_LINEAR_DMA_128x256) and d % 256:
+            with pytest.raises(RuntimeError):
+                pkg.linear_qkv_vt(x, w, bias, h, variant=variant)
+            continue
+        vt = torch.full((b, h, hd, row), float("nan"), device=cuda, dtype=torch.float16)
+        qkv, vt = pkg.linear_qkv_vt(x, w, bias, h, vt=vt, variant=variant)
+        assert torch.equal(qkv[..., :2 * d], full[..., :2 * d]), variant
+        assert torch.equal(vt[..., :s][..., pos], v), variant
+        assert torch.equal(vt[..., s:], torch.zeros_like(vt[..., s:])), variant
+
+
+@pytest.mark.parametrize("b,s,h", [(2, 96, 2), (1, 4160, 4), (1, 8224, 2)])
+def test_attention_vt_matches_ping_pong(pkg, cuda, b, s, h):
+    """Causal attention reading V transposed by the QKV GEMM: bitwise the
+    ping-pong kernel over the full projection (same scores, probabilities and
+    products; only the V fragment reads differ), and the FP32 reference."""
+    capi = pkg._capi
+    hd, d, k = 64, h * 64, 256
+    x = torch.randn(b, s, k, generator=_gen(3 * s + h)).half().to(cuda)
+    w = (torch.randn(3 * d, k, generator=_gen(s)) / k ** 0.5).half().to(cuda)
+    bias = (0.1 * torch.randn(3 * d, generator=_gen(h))).to(cuda)
+    full = pkg.linear(x, w, bias)
+    expected = pkg.attention(full, h, causal=True, variant=capi.XB_ATTN_PINGPONG)
+    qkv, vt = pkg.linear_qkv_vt(x, w, bias, h)
+    out = pkg.attention_vt(qkv, vt, h)
+    assert torch.equal(out, expected)
+    if s <= 4160:
+        ref = _attention_reference(full.cpu(), h, causal=True)
+        torch.testing.assert_close(out.cpu().float(), ref, atol=2e-3, rtol=1e-2)
+
+
+def test_qkv_vt_argument_errors(pkg, cuda):
+    """Shapes the transposed-V path does not take are refused before any launch."""
+    lib = pkg._capi.lib()
+    unsupported, bad_variant = -4, -10  # XB_ERR_UNSUPPORTED_SHAPE, XB_ERR_BAD_VARIANT
+    # seq_len not a multiple of 32, K % 64 != 0, head_dim other than 64 for the attention
+    assert lib.xb_linear_qkv_vt(None, None, None, None, None, 1, 100, 2, 64, 256, -1, None) == unsupported
+    assert lib.xb_linear_qkv_vt(None, None, None, None, None, 1, 96, 2, 64, 200, -1, None) == unsupported
+    assert lib.xb_attention_causal_vt(None, None, None, 1, 96, 2, 32, 0.1, None) == unsupported
+    assert lib.xb_attention_causal_vt(None, None, None, 1, 100, 2, 64, 0.1, None) == unsupported
+    # an NT tile, or a tile width that does not divide D
+    assert lib.xb_linear_qkv_vt(None, None, None, None, None, 1, 96, 2, 64, 256, 4, None) == bad_variant
+    assert lib.xb_linear_qkv_vt(None, None, None, None, None, 1, 96, 3, 64, 256, 0, None) == bad_variant
+
+
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("hd,b,s,h,variants", [
     (256, 2, 300, 2, ("XB_ATTN_W4_Q16", "XB_ATTN_W8_Q16")),
