@@ -86,6 +86,13 @@ def _dtype_code(dtype: torch.dtype, what: str) -> int:
         raise ValueError(f"{what}: unsupported dtype {dtype}") from None
 
 
+def _check_buffer(t: torch.Tensor, shape, dtype: torch.dtype, device: torch.device, what: str) -> None:
+    """A caller-supplied destination must be exactly what the kernel writes:
+    the kernels index it from the sizes of the other arguments."""
+    if tuple(t.shape) != tuple(shape) or t.dtype != dtype or t.device != device or not t.is_contiguous():
+        raise ValueError(f"{what} must be a contiguous {dtype} tensor of shape {tuple(shape)} on {device}")
+
+
 def _ptr(tensor: Optional[torch.Tensor]) -> Optional[int]:
     return None if tensor is None else tensor.data_ptr()
 
@@ -158,10 +165,14 @@ def fused_residual_layer_norm(
     if store_residual:
         if residual_out is None:
             residual_out = torch.empty_like(residual)
+        else:
+            _check_buffer(residual_out, residual.shape, torch.float32, residual.device, "residual_out")
     else:
         residual_out = None
     if norm_out is None:
         norm_out = torch.empty_like(residual, dtype=norm_dtype)
+    else:
+        _check_buffer(norm_out, residual.shape, norm_dtype, residual.device, "norm_out")
     rows = residual.numel() // n_cols
     upd_code, norm_code = _dtype_code(update.dtype, "update"), _dtype_code(norm_out.dtype, "norm")
     name = f"residual_layernorm_{n_cols}{'' if store_residual else '_final'}"
@@ -233,6 +244,8 @@ def linear(
     m = inputs.numel() // k
     if out is None:
         out = torch.empty((*inputs.shape[:-1], n), device=inputs.device, dtype=torch.float16)
+    else:
+        _check_buffer(out, (*inputs.shape[:-1], n), torch.float16, inputs.device, "out")
     epi = XB_EPI_BIAS_GELU if gelu else XB_EPI_BIAS
     check(
         _launch(f"gemm_n{n}_k{k}{'_gelu' if gelu else ''}", lambda: lib().xb_linear_v(
@@ -299,6 +312,8 @@ def attention(
         scale = head_dim ** -0.5
     if out is None:
         out = torch.empty((batch, seq_len, d_model), device=qkv.device, dtype=torch.float16)
+    else:
+        _check_buffer(out, (batch, seq_len, d_model), torch.float16, qkv.device, "out")
     valid = None if key_valid is None else _byte_mask(key_valid, batch * seq_len, qkv.device, "key_valid")
     name = f"attention_hd{head_dim}{'' if causal else '_full'}{'' if valid is None else '_masked'}"
     check(
@@ -349,11 +364,15 @@ def linear_qkv_vt(
     if weight.shape[1] != k or n % (3 * num_heads) != 0:
         raise ValueError("weight must be [3 * num_heads * head_dim, K]")
     head_dim = n // (3 * num_heads)
+    vt_shape = (batch, num_heads, head_dim, vt_row_stride(seq_len))
     if out is None:
         out = torch.empty((batch, seq_len, n), device=inputs.device, dtype=torch.float16)
+    else:
+        _check_buffer(out, (batch, seq_len, n), torch.float16, inputs.device, "out")
     if vt is None:
-        vt = torch.empty((batch, num_heads, head_dim, vt_row_stride(seq_len)), device=inputs.device,
-                         dtype=torch.float16)
+        vt = torch.empty(vt_shape, device=inputs.device, dtype=torch.float16)
+    else:
+        _check_buffer(vt, vt_shape, torch.float16, inputs.device, "vt")
     check(
         _launch(f"gemm_n{n}_k{k}_vt", lambda: lib().xb_linear_qkv_vt(
             inputs.data_ptr(), weight.data_ptr(), _ptr(bias), out.data_ptr(), vt.data_ptr(), batch, seq_len,
@@ -379,12 +398,15 @@ def attention_vt(
     batch, seq_len, width = qkv.shape
     d_model = width // 3
     head_dim = d_model // num_heads
-    if tuple(vt.shape) != (batch, num_heads, head_dim, vt_row_stride(seq_len)) or vt.dtype != torch.float16:
-        raise ValueError("vt must be the [B, H, head_dim, vt_row_stride(S)] float16 buffer of linear_qkv_vt")
+    if qkv.dtype != torch.float16 or not qkv.is_contiguous():
+        raise ValueError("qkv must be contiguous float16")
+    _check_buffer(vt, (batch, num_heads, head_dim, vt_row_stride(seq_len)), torch.float16, qkv.device, "vt")
     if scale is None:
         scale = head_dim ** -0.5
     if out is None:
         out = torch.empty((batch, seq_len, d_model), device=qkv.device, dtype=torch.float16)
+    else:
+        _check_buffer(out, (batch, seq_len, d_model), torch.float16, qkv.device, "out")
     check(
         _launch(f"attention_hd{head_dim}_vt", lambda: lib().xb_attention_causal_vt(
             qkv.data_ptr(), vt.data_ptr(), out.data_ptr(), batch, seq_len, num_heads, head_dim, float(scale),
@@ -455,6 +477,8 @@ def attention_kv_cache(
     d_model = num_heads * head_dim
     if out is None:
         out = torch.empty((batch, chunk, d_model), device=qkv.device, dtype=torch.float16)
+    else:
+        _check_buffer(out, (batch, chunk, d_model), torch.float16, qkv.device, "out")
     if no_alloc:
         with torch.cuda.device(qkv.device):
             check(
@@ -549,6 +573,11 @@ def fused_forward_d128(
     batch, seq_len, _ = x.shape
     if out is None:
         out = torch.empty_like(x)
+    else:
+        _check_buffer(out, x.shape, torch.float32, x.device, "out")
+    # the packed parameters of num_layers layers (UserOptimizedTransformer._fused_stack_parameters)
+    _check_buffer(wpack, (num_layers * 128 * (4 * 128 + 2 * ffn_dim),), torch.float16, x.device, "wpack")
+    _check_buffer(ppack, (num_layers * (9 * 128 + ffn_dim) + 2 * 128,), torch.float32, x.device, "ppack")
     valid = None if token_valid is None else _byte_mask(token_valid, batch * seq_len, x.device, "token_valid")
     ws = fused_split_workspace(x.device, batch, seq_len, num_heads, num_layers, causal) if split else None
     ws_bytes = 0 if ws is None else ws.numel()

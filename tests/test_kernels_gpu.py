@@ -251,6 +251,34 @@ def test_attention_vt_matches_ping_pong(pkg, cuda, b, s, h):
         torch.testing.assert_close(out.cpu().float(), ref, atol=2e-3, rtol=1e-2)
 
 
+def test_wrong_destination_buffers_are_refused(pkg, cuda):
+    """Caller-supplied destinations are checked against what the kernel writes
+    (shape, dtype, device, contiguity) before anything is launched."""
+    kernels = __import__(pkg.__name__ + ".kernels", fromlist=["linear"])
+    x = torch.randn(2, 64, 256, device=cuda).half()
+    w = torch.randn(3 * 256, 256, device=cuda).half()
+    with pytest.raises(ValueError):
+        pkg.linear(x, w, None, out=torch.empty(2, 64, 3 * 256 - 8, device=cuda, dtype=torch.float16))
+    with pytest.raises(ValueError):
+        pkg.linear(x, w, None, out=torch.empty(2, 64, 3 * 256, device=cuda, dtype=torch.float32))
+    qkv = pkg.linear(x, w, None)
+    with pytest.raises(ValueError):
+        pkg.attention(qkv, 4, out=torch.empty(2, 63, 256, device=cuda, dtype=torch.float16))
+    with pytest.raises(ValueError):
+        pkg.attention(qkv, 4, out=torch.empty(2, 256, 64, device=cuda, dtype=torch.float16).transpose(1, 2))
+    with pytest.raises(ValueError):
+        pkg.linear_qkv_vt(x, w, None, 4, vt=torch.empty(2, 4, 64, 32, device=cuda, dtype=torch.float16))
+    r = torch.randn(2, 64, 256, device=cuda)
+    g, b = torch.ones(256, device=cuda), torch.zeros(256, device=cuda)
+    with pytest.raises(ValueError):
+        pkg.fused_residual_layer_norm(r, x, g, b, 1e-5, torch.float16,
+                                      norm_out=torch.empty(2, 64, 256, device=cuda, dtype=torch.float32))
+    xs = torch.randn(1, 16, 128, device=cuda)
+    with pytest.raises(ValueError):  # the packed weights of one layer passed for two
+        kernels.fused_forward_d128(xs, torch.empty(6 * 128 * 128, device=cuda, dtype=torch.float16),
+                                   torch.empty(9 * 128 + 128 + 256, device=cuda), 4, 128, 2)
+
+
 def test_qkv_vt_argument_errors(pkg, cuda):
     """Shapes the transposed-V path does not take are refused before any launch."""
     lib = pkg._capi.lib()
