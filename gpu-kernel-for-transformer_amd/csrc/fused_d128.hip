@@ -26,8 +26,10 @@
 // xb_pack_linear_fragments), fragment-major: one 16 x 32 fragment is 1 KB,
 // 16 bytes per lane.  Q and the attention context stay in registers in that
 // operand order; K is written to LDS with each k-step's 32 features in the
-// same order, V transposed.  LN outputs and the FFN hidden activation never
-// leave registers.
+// same order, V transposed (in the head_dim <= 64 kernel with each 32-key
+// step's columns in the P operand's key order, so one 16-byte read is one
+// operand fragment).  LN outputs and the FFN hidden activation never leave
+// registers.
 //
 // Weights.  Every weight matrix (128 x 128 FP16, 32 KB) is copied once per
 // workgroup into one of two LDS stages by direct global -> LDS loads (4 per
@@ -570,8 +572,8 @@ __device__ __forceinline__ void attend16(const half_t* k_lds, const half_t* vt_l
         for (int i = 0; i < 4; ++i) cop[c / 2][4 * (c & 1) + i] = v[i];
       }
     }
-    // Narrow heads: interleaving more than two of them only raises register
-    // pressure past the 128 VGPRs of four waves per SIMD (and spills).
+    // Narrow heads: the scheduler may interleave two of them; four or eight
+    // measured no faster.
     if constexpr (HD <= 16) {
       if (hh % 2 == 1) __builtin_amdgcn_sched_barrier(0);
     }
