@@ -115,6 +115,28 @@ def test_pack_linear_fragments_layout(pkg, cuda):
         assert torch.equal(packed, expect), f"natural={natural}"
 
 
+def test_transposed_v_forward_matches_plain_plan(pkg, cuda):
+    """A long head_dim-64 causal forward takes V transposed from the QKV GEMM
+    (plan: flash_pingpong_vt); the same model with the plan resolved without
+    it (plain QKV GEMM + ping-pong attention) gives the same output bit for
+    bit, here at S = 4128 (rows padded to 4160)."""
+    capi = pkg._capi
+    config = pkg.TransformerConfig(2, 4128, 1024, 16, 1024, 2, True)
+    _, optimized = _models(pkg, config, cuda)
+    x = torch.randn(2, 4128, 1024, generator=torch.Generator(device=cuda).manual_seed(11), device=cuda)
+    plan = optimized.execution_plan(2, 4128)
+    assert plan.attention_variant == capi.XB_ATTN_PINGPONG_VT and "flash_pingpong_vt" in plan.describe()
+    with torch.inference_mode():
+        out_vt = optimized(x).clone()
+    key = next(k for k, v in optimized._plans.items() if v is plan)
+    optimized._plans[key] = pkg.resolve_shape_execution_plan(config, 2, 4128, transposed_v_allowed=False)
+    assert optimized._plans[key].attention_variant == capi.XB_ATTN_PINGPONG
+    with torch.inference_mode():
+        out_plain = optimized(x)
+    assert torch.equal(out_vt, out_plain)
+    assert bool(torch.isfinite(out_vt).all())
+
+
 def test_config5_official_size(pkg, cuda):
     """Official shape 14 unchanged (B=32, S=100000, D=1024, 16 heads, 2 layers).
 
