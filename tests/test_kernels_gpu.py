@@ -231,7 +231,7 @@ def test_linear_qkv_vt_layout(pkg, cuda, b, s, h, k):
         assert torch.equal(vt[..., s:], torch.zeros_like(vt[..., s:])), variant
 
 
-@pytest.mark.parametrize("b,s,h", [(2, 96, 2), (1, 4160, 4), (1, 8224, 2)])
+@pytest.mark.parametrize("b,s,h", [(3, 32, 2), (2, 96, 2), (1, 4160, 4), (1, 8224, 2)])
 def test_attention_vt_matches_ping_pong(pkg, cuda, b, s, h):
     """Causal attention reading V transposed by the QKV GEMM: bitwise the
     ping-pong kernel over the full projection (same scores, probabilities and

@@ -34,11 +34,14 @@ def _runners(pkg):
     return graphs, chunks, kernels
 
 
-@pytest.mark.parametrize("geom", [(2, 64, 256, 4, 512, 2), (16, 128, 128, 4, 128, 2), (3, 200, 1024, 16, 1024, 1)])
+@pytest.mark.parametrize("geom", [(2, 64, 256, 4, 512, 2), (16, 128, 128, 4, 128, 2), (3, 200, 1024, 16, 1024, 1),
+                                  (1, 4128, 1024, 16, 1024, 1)])
 def test_fixed_input_graph_replays_bitwise(pkg, cuda, geom):
-    """Per-op, split whole-stack and D=1024 forwards captured; replays with eager
-    work (and eager forwards of the same model) between them equal eager;
-    another input or an in-place change to the captured one runs eagerly."""
+    """Per-op, split whole-stack, D=1024 and long (transposed-V attention, its
+    V^T buffer allocated inside the capture) forwards captured; replays with
+    eager work (and eager forwards of the same model) between them equal
+    eager; another input or an in-place change to the captured one runs
+    eagerly."""
     graphs, _, kernels = _runners(pkg)
     config = pkg.TransformerConfig(*geom, True)
     _, optimized = _models(pkg, config, cuda)
