@@ -37,6 +37,16 @@ __device__ __forceinline__ int xcd_contiguous_tile(int b, int nb) {
   return x * q + (x < r ? x : r) + b / 8;
 }
 
+// FP32 -> FP16 of an epilogue value, rounded once from the FP32 value.  The
+// empty asm pins the FP32 result: otherwise the backend may fold the last
+// multiply or add into a singly-rounded v_fma_mix conversion in some tile
+// instantiations and not others, and the FP16 output would then depend on
+// the tile (hence on the batch size that selected it).
+__device__ __forceinline__ half_t to_half_pinned(float v) {
+  asm volatile("" : "+v"(v));
+  return (half_t)v;
+}
+
 template <int BM, int BN, int WGM, int WGN, int EPI>
 __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_nt_kernel(
     const half_t* __restrict__ A, const half_t* __restrict__ W,
@@ -135,7 +145,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_nt_kernel(
       for (int e = 0; e < 4; ++e) {
         float v = acc[i][j][e] + bv;
         if constexpr (EPI == XB_EPI_BIAS_GELU) v = gelu_erf(v);
-        cs[(wm + 16 * i + (lane / 16) * 4 + e) * LDC + c] = (half_t)v;
+        cs[(wm + 16 * i + (lane / 16) * 4 + e) * LDC + c] = to_half_pinned(v);
       }
   }
   __syncthreads();
@@ -312,7 +322,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_kernel(
           const int r = wm + 16 * i + lane % 16;
           const int p = (r & ~31) | (((r & 15) >> 2) << 3) | (((r >> 4) & 1) << 2) | (r & 3);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) vs[(col + e) * BM + p] = (half_t)(acc[i][j][e] + b[e]);
+          for (int e = 0; e < 4; ++e) vs[(col + e) * BM + p] = to_half_pinned(acc[i][j][e] + b[e]);
         }
       }
       slab_barrier();
@@ -355,7 +365,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_kernel(
       for (int e = 0; e < 4; ++e) {
         float v = acc[i][j][e] + b[e];
         if constexpr (EPI == XB_EPI_BIAS_GELU) v = gelu_erf(v);
-        h[e] = (half_t)v;
+        h[e] = to_half_pinned(v);
       }
       *reinterpret_cast<half4_t*>(cs + row * BN + 8 * ((col / 8) ^ (row & SW)) + (col & 7)) = h;
     }

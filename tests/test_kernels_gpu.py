@@ -103,7 +103,10 @@ def test_linear(pkg, cuda, m, n, k, gelu):
 def test_linear_every_variant(pkg, cuda, m, n, k, gelu):
     """Every tile variant the plan can name (xb_linear_v), forced on shapes all
     of them accept, against the FP32 reference; a variant not built for the
-    shape is refused."""
+    shape is refused.  The plan picks the tile from the row count, so a
+    batch's rows must not depend on it: every direct-to-LDS tile gives the
+    same output bit for bit, and so does every register-staged tile (same
+    K order; each epilogue rounds the FP32 result to FP16 once)."""
     capi = pkg._capi
     a = torch.randn(m, k, generator=_gen(m + k)).half()
     w = (torch.randn(n, k, generator=_gen(n)) * k**-0.5).half()
@@ -112,11 +115,17 @@ def test_linear_every_variant(pkg, cuda, m, n, k, gelu):
     if gelu:
         ref = F.gelu(ref, approximate="none")
     ag, wg, bg = a.to(cuda), w.to(cuda), bias.to(cuda)
+    outs = {}
     for variant in (capi.XB_LINEAR_DMA_256x256, capi.XB_LINEAR_DMA_256x192, capi.XB_LINEAR_DMA_128x256,
                     capi.XB_LINEAR_DMA_128x128, capi.XB_LINEAR_NT_128x128, capi.XB_LINEAR_NT_64x64):
         out = pkg.linear(ag, wg, bg, gelu=gelu, variant=variant)
         torch.testing.assert_close(out.cpu().float(), ref, atol=2e-3, rtol=2e-3,
                                    msg=lambda e, v=variant: f"variant {v}: {e}")
+        outs[variant] = out
+    dma = [capi.XB_LINEAR_DMA_256x256, capi.XB_LINEAR_DMA_256x192, capi.XB_LINEAR_DMA_128x256, capi.XB_LINEAR_DMA_128x128]
+    for v in dma[1:]:
+        assert torch.equal(outs[v], outs[dma[0]]), f"variant {v} differs from {dma[0]}"
+    assert torch.equal(outs[capi.XB_LINEAR_NT_64x64], outs[capi.XB_LINEAR_NT_128x128])
     with pytest.raises(RuntimeError, match="code -10"):  # 256x192 needs N % 192 == 0
         pkg.linear(ag[:, :k], wg[:n - 128], None, variant=capi.XB_LINEAR_DMA_256x192)
 

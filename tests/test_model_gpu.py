@@ -128,6 +128,9 @@ def test_transposed_v_forward_matches_plain_plan(pkg, cuda):
     assert plan.attention_variant == capi.XB_ATTN_PINGPONG_VT and "flash_pingpong_vt" in plan.describe()
     with torch.inference_mode():
         out_vt = optimized(x).clone()
+        optimized._large_batch_chunk_size = 1  # one sequence per slice, each with its own V^T buffer
+        assert torch.equal(optimized(x), out_vt)
+        optimized._large_batch_chunk_size = 0
     key = next(k for k, v in optimized._plans.items() if v is plan)
     optimized._plans[key] = pkg.resolve_shape_execution_plan(config, 2, 4128, transposed_v_allowed=False)
     assert optimized._plans[key].attention_variant == capi.XB_ATTN_PINGPONG
