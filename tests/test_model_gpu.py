@@ -220,6 +220,24 @@ def test_batch_chunking_matches_unchunked(pkg, cuda):
     assert torch.equal(whole, chunked)
 
 
+@pytest.mark.parametrize("geom", [(64, 128, 1024, 4, 1024, 1), (3, 200, 512, 8, 2048, 1)])
+def test_per_op_rows_do_not_depend_on_the_batch(pkg, cuda, geom):
+    """Batch elements are independent (README.md:260-263): a D >= 256 forward
+    of the whole batch equals forwards of single sequences bit for bit, though
+    the GEMM tiles (chosen from the row count) and the head_dim-256 attention
+    form (chosen from B * H) differ between the two."""
+    config = pkg.TransformerConfig(*geom, True)
+    _, optimized = _models(pkg, config, cuda)
+    x, _ = generate_random_case(config, torch.device("cpu"), torch.float32, seed=13)
+    xg = x.to(cuda)
+    b = config.batch_size
+    assert optimized.execution_plan(b, config.seq_len).describe() != optimized.execution_plan(1, config.seq_len).describe()
+    with torch.inference_mode():
+        whole = optimized(xg)
+        for i in (0, b // 2, b - 1):
+            assert torch.equal(optimized(xg[i:i + 1]), whole[i:i + 1]), f"sequence {i}"
+
+
 def test_graph_replay_matches_eager(pkg, cuda):
     """Capture the forward in a HIP graph; every replay equals the eager output bitwise."""
     config = pkg.OFFICIAL_BENCHMARK_SHAPES[1]
