@@ -4,8 +4,11 @@
 // biased variance of the centred row, y = (x - mean) * rsqrt(var + eps), with
 // the optional affine transform.  The reference launches one program per row
 // (triton_fused_norm.py:159-169); here a row belongs to a group of LPR lanes of
-// one wave, each lane owning 8 consecutive columns per chunk, so every global
-// access is a 16- or 32-byte vector and both reductions are wave shuffles.
+// one wave, each lane owning 4 (rows of 256 columns and more) or 8 consecutive
+// columns per chunk, so every global access is an 8- to 32-byte vector, and
+// both reductions are wave shuffles.
+#include <type_traits>
+
 #include "common.h"
 #include "../../include/xblock.h"
 
@@ -46,20 +49,52 @@ struct Vec8<half_t> {
   }
 };
 
-// D = CH * LPR * 8 columns; 256 / LPR rows per 256-thread block.
+template <typename T>
+struct Vec4;
+
+template <>
+struct Vec4<float> {
+  __device__ static void load(const float* p, float v[4]) {
+    const float4_t a = *reinterpret_cast<const float4_t*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = a[i];
+  }
+  __device__ static void store(float* p, const float v[4]) {
+    *reinterpret_cast<float4_t*>(p) = float4_t{v[0], v[1], v[2], v[3]};
+  }
+};
+
+template <>
+struct Vec4<half_t> {
+  __device__ static void load(const half_t* p, float v[4]) {
+    const half4_t a = *reinterpret_cast<const half4_t*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = (float)a[i];
+  }
+  __device__ static void store(half_t* p, const float v[4]) {
+    *reinterpret_cast<half4_t*>(p) = half4_t{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
+  }
+};
+
+// A lane's VEC consecutive columns per chunk (VEC = 4 or 8).
+template <int VEC, typename T>
+using VecIO = typename std::conditional<VEC == 8, Vec8<T>, Vec4<T>>::type;
+
+// D = CH * LPR * VEC columns (chunk c of lane l: columns VEC (c LPR + l) on);
+// 256 / LPR rows per 256-thread block.
 // RES: add `upd` to `x` first and (when res_out != nullptr) store the sum.
 // row_valid (optional, one byte per row) with mask_mode bits
 // XB_MASK_UPDATE / XB_MASK_SUM / XB_MASK_OUTPUT zeroes, for rows whose byte
 // is 0, the update, the sum (stored residual and LayerNorm input), or the
 // output (by selection, so NaN in a masked update does not leak).
-template <int D, int LPR, bool RES, typename TU, typename TY>
+template <int D, int LPR, int VEC, bool RES, typename TU, typename TY>
 __global__ __launch_bounds__(256) void ln_rows_kernel(
     const float* x, const TU* __restrict__ upd,
     const float* __restrict__ gamma, const float* __restrict__ beta,
     float* res_out, TY* __restrict__ y, int64_t rows, float eps, int affine,
     const uint8_t* __restrict__ row_valid, int mask_mode) {
-  constexpr int CH = D / (LPR * 8);
-  static_assert(CH * LPR * 8 == D, "row width must split into 8-column lanes");
+  constexpr int CH = D / (LPR * VEC);
+  static_assert(CH * LPR * VEC == D, "row width must split into VEC-column lanes");
   constexpr int RPB = 256 / LPR;
   const int lr = threadIdx.x % LPR;
   const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / LPR;
@@ -71,29 +106,29 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(
   const bool drop_sum = invalid && (mask_mode & XB_MASK_SUM);
   const bool drop_out = invalid && (mask_mode & XB_MASK_OUTPUT);
 
-  float v[CH][8];
+  float v[CH][VEC];
   const float* xr = x + row * D;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
-    const int col = (c * LPR + lr) * 8;
-    Vec8<float>::load(xr + col, v[c]);
+    const int col = (c * LPR + lr) * VEC;
+    VecIO<VEC, float>::load(xr + col, v[c]);
     if constexpr (RES) {
       if (!drop_update) {
-        float u[8];
-        Vec8<TU>::load(upd + row * D + col, u);
+        float u[VEC];
+        VecIO<VEC, TU>::load(upd + row * D + col, u);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[c][i] += u[i];
+        for (int i = 0; i < VEC; ++i) v[c][i] += u[i];
       }
     }
     if (drop_sum) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[c][i] = 0.f;
+      for (int i = 0; i < VEC; ++i) v[c][i] = 0.f;
     }
   }
   if constexpr (RES) {
     if (res_out != nullptr) {
 #pragma unroll
-      for (int c = 0; c < CH; ++c) Vec8<float>::store(res_out + row * D + (c * LPR + lr) * 8, v[c]);
+      for (int c = 0; c < CH; ++c) VecIO<VEC, float>::store(res_out + row * D + (c * LPR + lr) * VEC, v[c]);
     }
   }
 
@@ -101,13 +136,13 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(
 #pragma unroll
   for (int c = 0; c < CH; ++c)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) s += v[c][i];
+    for (int i = 0; i < VEC; ++i) s += v[c][i];
   const float mean = group_sum<LPR>(s) * (1.0f / D);
   float q = 0.f;
 #pragma unroll
   for (int c = 0; c < CH; ++c)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < VEC; ++i) {
       v[c][i] -= mean;
       q += v[c][i] * v[c][i];
     }
@@ -115,23 +150,23 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(
 
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
-    const int col = (c * LPR + lr) * 8;
-    float o[8];
+    const int col = (c * LPR + lr) * VEC;
+    float o[VEC];
     if (affine) {
-      float g[8], b[8];
-      Vec8<float>::load(gamma + col, g);
-      Vec8<float>::load(beta + col, b);
+      float g[VEC], b[VEC];
+      VecIO<VEC, float>::load(gamma + col, g);
+      VecIO<VEC, float>::load(beta + col, b);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = v[c][i] * rstd * g[i] + b[i];
+      for (int i = 0; i < VEC; ++i) o[i] = v[c][i] * rstd * g[i] + b[i];
     } else {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = v[c][i] * rstd;
+      for (int i = 0; i < VEC; ++i) o[i] = v[c][i] * rstd;
     }
     if (drop_out) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = 0.f;
+      for (int i = 0; i < VEC; ++i) o[i] = 0.f;
     }
-    Vec8<TY>::store(y + row * D + col, o);
+    VecIO<VEC, TY>::store(y + row * D + col, o);
   }
 }
 
@@ -198,6 +233,10 @@ __global__ __launch_bounds__(256) void ln_generic_kernel(
   }
 }
 
+// Rows of 256 columns and more: 4-column lanes (FP32 rows 1 KB and up:
+// 8192 x 1024 residual + LayerNorm 17.6 -> 16.5 us, 3.2M x 1024 7.5 -> 7.1 ms
+// against 8-column lanes); shorter rows keep 8-column lanes (D = 128: 331
+// against 337 us for 1.28M rows).
 template <int D, int LPR, bool RES, typename TU, typename TY>
 static hipError_t launch_rows(const float* x, const void* upd, const float* g,
                               const float* b, float* res_out, void* y,
@@ -205,7 +244,8 @@ static hipError_t launch_rows(const float* x, const void* upd, const float* g,
                               const uint8_t* rv, int mm, hipStream_t s) {
   constexpr int RPB = 256 / LPR;
   const int64_t blocks = (rows + RPB - 1) / RPB;
-  hipLaunchKernelGGL((ln_rows_kernel<D, LPR, RES, TU, TY>), dim3((unsigned)blocks),
+  constexpr int VEC = D >= 256 ? 4 : 8;
+  hipLaunchKernelGGL((ln_rows_kernel<D, LPR, VEC, RES, TU, TY>), dim3((unsigned)blocks),
                      dim3(256), 0, s, x, static_cast<const TU*>(upd), g, b,
                      res_out, static_cast<TY*>(y), rows, eps, affine, rv, mm);
   return hipGetLastError();
