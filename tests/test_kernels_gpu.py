@@ -37,7 +37,7 @@ def test_layer_norm(pkg, cuda, rows, cols, out_dtype, affine):
         torch.testing.assert_close(y.cpu().float(), ref.half().float(), atol=2e-3, rtol=1e-3)
 
 
-@pytest.mark.parametrize("cols", [128, 1024, 96])
+@pytest.mark.parametrize("cols", [64, 128, 256, 512, 1024, 2048, 96])  # 8- and 4-column lanes, generic
 @pytest.mark.parametrize("upd_dtype", [F16, F32])
 @pytest.mark.parametrize("mode", ["store", "inplace", "nostore_f32"])
 def test_fused_residual_layer_norm(pkg, cuda, cols, upd_dtype, mode):
