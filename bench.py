@@ -19,15 +19,23 @@ Printed as ONE JSON line with, besides the driver's fields:
                   bounded sample of the same workload, on all of this host's
                   cores (len(os.sched_getaffinity(0)) threads)
   accuracy        the reference's rule (TTB:1237-1304) on the GPU output against
-                  the oracle: whole batch for every config but cfg5, whose
-                  causal 4096-token prefix is checked on its first, middle and
-                  last sequences (all 32 with --full-accuracy); every config's
-                  whole output must also be finite (streamed_shape14.py:167-169)
+                  the oracle: the timed input's whole batch for every config
+                  but cfg5, whose causal 4096-token prefix is checked on its
+                  first, middle and last sequences (all 32 with
+                  --full-accuracy), plus the reference's seeded trials
+                  (inputs from seeds 1234+t, 5 by default; 2 on sampled
+                  sequences for cfg2 and cfg5); every config's whole output
+                  must also be finite (streamed_shape14.py:167-169) and no
+                  split-form K/V hand-off may have failed
   per_config      all five BASELINE configs: tokens/s, ms, execution plan,
                   dominant-kernel roofline, forward roofline, accuracy; cfg2
                   also times the reference's own shape-6 form (chunks of 1024
                   with a hipGraph per chunk shape, TTB:1740, :1826-1846)
   decode          KV-cached single-token steps at cfg5's geometry
+Timed call: forward(x, all-True mask), the reference harness's (TTB:1478-1491);
+each config also reports the reference harness's per-call statistics
+(median/mean/p90/min over 3 rounds of 100 calls, TTB:1426-1552) and its
+measured peak device memory (streamed_shape14.py:174-175).
 Timing: before the --warmup steps of every timed region, the step runs untimed
 until --settle seconds of wall time have passed (default 0.1).  An MI355X
 leaving idle needs about 30 ms of load before its clock settles: after 2 s
@@ -87,15 +95,21 @@ def parse_args(argv=None):
                    help="seconds of untimed steps before the warm-up steps of each timed region (GPU clock ramp)")
     p.add_argument("--batch", type=int, default=0,
                    help="run the headline with this batch instead of the shape's (the line then says so)")
-    p.add_argument("--accuracy-trials", type=int, default=1,
-                   help="accuracy samples: the timed input, then fresh inputs seeded 1234+t (TTB:1307-1372)")
+    p.add_argument("--accuracy-trials", type=int, default=5,
+                   help="seeded accuracy trials per config, inputs seeded 1234+t, t < trials, as the reference's "
+                        "harness (TTB:1307-1372, default 5, TTB:1618); the batch-heavy cfg2 and the long cfg5 run "
+                        "min(trials, 2) of them on sampled sequences")
+    p.add_argument("--ref-repeats", type=int, default=100,
+                   help="reference-harness timing: per-call HIP-event samples per round (TTB:1426-1452, default "
+                        "100 as TTB:1622); sequences longer than 8192 take 2")
+    p.add_argument("--ref-rounds", type=int, default=3, help="reference-harness timing rounds (TTB:1623)")
     p.add_argument("--full-accuracy", action="store_true", help="cfg5: check all 32 sequences' prefixes")
     p.add_argument("--strict-accuracy", action="store_true", help="exit with status 2 when an accuracy check fails")
     p.add_argument("--memory-fraction", type=float, default=0.9,
                    help="skip a config whose device-memory estimate exceeds this fraction of the GPU")
     args = p.parse_args(argv)
     if (args.steps <= 0 or args.warmup < 0 or args.rounds <= 0 or args.accuracy_trials <= 0 or args.batch < 0
-            or args.settle < 0):
+            or args.settle < 0 or args.ref_repeats <= 0 or args.ref_rounds <= 0):
         p.error("steps, rounds and accuracy trials must be positive; warmup, settle and batch non-negative")
     if not 0 < args.memory_fraction <= 1:
         p.error("--memory-fraction must be in (0, 1]")
@@ -428,21 +442,45 @@ def main(argv=None) -> int:
             results.append(compare_outputs(ref, out[:, :prefix].index_select(0, idx).cpu()))
         return results
 
-    def extra_trials(baseline, model, config, rows, trials):
-        """Accuracy of fresh inputs seeded 1234+t, t = 1..trials-1, on `rows` sequences."""
-        from oracle.accuracy import compare_outputs
+    def seeded_trials(baseline, model, config, trials, rows):
+        """The reference's accuracy trials (TTB:1307-1372): for t < trials, the
+        full-size input generate_random_case draws on the GPU from seed 1234+t
+        (x ~ N(0,1), all-True mask), one forward of the whole batch, checked
+        against the oracle on `rows` sequences (causal prefix for long ones)."""
+        from oracle.baseline import generate_random_case
 
         results = []
-        for t in range(1, trials):
-            g = torch.Generator(device=device).manual_seed(1234 + t)
-            xt = torch.randn(rows, config.seq_len, config.d_model, generator=g, device=device)
+        for t in range(trials):
+            xt, mt = generate_random_case(config, device, torch.float32, seed=1234 + t)
             with torch.inference_mode():
-                out_t = model(xt)
-                if config.seq_len > 8192:  # long context: causal prefix only
-                    xt, out_t = xt[:, :LONG_PREFIX], out_t[:, :LONG_PREFIX]
-                ref_t = baseline(xt.float().cpu().contiguous())
-            results.append(compare_outputs(ref_t, out_t.cpu()))
+                out_t = model(xt, mt)
+                torch.cuda.synchronize()
+            results += check_rows(baseline, config, out_t, xt, rows)
+            del xt, mt, out_t
         return results
+
+    def reference_timing(run, repeats, rounds):
+        """The reference harness's latency statistics (TTB:1426-1452, :1507-1552):
+        per-call HIP events around each call, `repeats` calls per round."""
+        samples = []
+        for _ in range(rounds):
+            starts = [torch.cuda.Event(enable_timing=True) for _ in range(repeats)]
+            ends = [torch.cuda.Event(enable_timing=True) for _ in range(repeats)]
+            torch.cuda.synchronize()
+            for i in range(repeats):
+                starts[i].record()
+                run()
+                ends[i].record()
+            torch.cuda.synchronize()
+            samples += [a.elapsed_time(b) for a, b in zip(starts, ends)]
+        ordered = sorted(samples)
+        pos = (len(ordered) - 1) * 0.9
+        lo, hi = int(pos), min(int(pos) + 1, len(ordered) - 1)
+        p90 = ordered[lo] * (1.0 - (pos - lo)) + ordered[hi] * (pos - lo)
+        return {"median_ms": statistics.median(samples), "mean_ms": statistics.fmean(samples), "p90_ms": p90,
+                "min_ms": ordered[0], "samples": len(samples), "rounds": rounds,
+                "note": "per-call HIP events as the reference's benchmark_once (TTB:1426-1452); includes each "
+                        "call's host issue time when the GPU is idle"}
 
     def cpu_leg(baseline, config, x_gpu, budget_s, rows_per_call):
         """The oracle on the host cores over a bounded slice: tokens/s."""
@@ -466,22 +504,34 @@ def main(argv=None) -> int:
             f" (causal prefix {prefix} of S={config.seq_len})" if prefix else "")
         return {"value": tokens / elapsed, "unit": "tokens/s", "cores": threads, "kind": "port", "sample": sample}
 
-    def kernel_profile(model, x, config, tokens, reps, lead=0):
+    def kernel_profile(model, x, mask, config, tokens, reps, step_ms, lead=0):
+        """Per-kernel average launch time from HIP events around each launch.
+
+        A forward that is one launch has its kernel time bounded by the step
+        time (back-to-back launches between two events, no per-launch event
+        overhead); the events around a single tens-of-microseconds launch
+        read several percent long, so such a kernel takes the smaller of the
+        two and says which it used."""
         with torch.inference_mode():
             # `lead` unrecorded forwards first, with no synchronisation after them:
             # the host then runs ahead of the GPU, so the events around a short
             # kernel time the kernel and not the host's issue gaps.
             for _ in range(lead):
-                model(x)
+                model(x, mask)
             with kernels.LaunchRecorder() as rec:
                 for _ in range(reps):
-                    model(x)
+                    model(x, mask)
         torch.cuda.synchronize()
+        durations = rec.durations_ms()
+        one_launch = len(durations) == 1 and len(next(iter(durations.values()))) == reps
         per = {}
-        for kname, durs in rec.durations_ms().items():
+        for kname, durs in durations.items():
             avg = statistics.fmean(durs)
+            source = "hip_events_per_launch"
+            if one_launch and step_ms < avg:
+                avg, source = step_ms, "step_time (one launch per forward)"
             b_, f_ = kernel_costs(kname, config, tokens)
-            per[kname] = {"avg_ms": avg, "launches_per_step": len(durs) // reps,
+            per[kname] = {"avg_ms": avg, "launches_per_step": len(durs) // reps, "time_source": source,
                           "share_ms": avg * len(durs) / reps, **roofline_of(max(b_, 1.0), f_, avg / 1e3),
                           "bytes_per_launch": b_, "flops_per_launch": f_}
         dominant = max(per, key=lambda k: per[k]["share_ms"])
@@ -520,7 +570,7 @@ def main(argv=None) -> int:
         try:
             entry_, head_extra = run_config(
                 args, pkg, config, shape_id, name, is_head, build, make_input, time_steps, check_rows,
-                extra_trials, cpu_leg, kernel_profile, graphs, chunking)
+                seeded_trials, reference_timing, cpu_leg, kernel_profile, graphs, chunking, kernels, device)
         except torch.cuda.OutOfMemoryError as error:
             torch.cuda.empty_cache()
             reason = f"SAFE_ABORT: out of device memory: {str(error).splitlines()[0]}"
@@ -606,13 +656,30 @@ def main(argv=None) -> int:
     return 0
 
 
+def trial_rows(config):
+    """Sequences each seeded trial checks: every one for the small configs;
+    1024 (first, middle and last ranges) for a batch of 10,000; the first,
+    middle and last for long sequences (causal prefix)."""
+    b = config.batch_size
+    if config.seq_len > 8192:
+        return sorted({0, b // 2, b - 1})
+    if b * config.seq_len >= 1_000_000:
+        third = 1024 // 3
+        return sorted(set(range(third)) | set(range(b // 2, b // 2 + third)) | set(range(b - (1024 - 2 * third), b)))
+    return list(range(b))
+
+
 def run_config(args, pkg, config, shape_id, name, is_head, build, make_input, time_steps, check_rows,
-               extra_trials, cpu_leg, kernel_profile, graphs, chunking):
+               seeded_trials, reference_timing, cpu_leg, kernel_profile, graphs, chunking, kernels, device):
     """Time one config, profile its kernels, check it; returns (per-config entry, headline extras)."""
     import torch
 
+    torch.cuda.reset_peak_memory_stats(device)
     baseline, model = build(config)
     x = make_input(config, 1234 + 100000)
+    # The reference times its fixed input with the mask generate_random_case
+    # gives at padding_ratio 0: all True (TTB:1478-1491, TTB:1615).
+    mask = torch.ones(config.batch_size, config.seq_len, device=device, dtype=torch.bool)
     tokens = config.batch_size * config.seq_len
     big = config.seq_len > 8192
     if big:
@@ -622,15 +689,16 @@ def run_config(args, pkg, config, shape_id, name, is_head, build, make_input, ti
         # (the repeat counts the reference's harness suggests).
         steps, warmup = (args.steps, args.warmup) if is_head else (100, 20)
     plan = model.execution_plan(config.batch_size, config.seq_len)
+    failures_before = kernels.split_handoff_failures(device)
     with torch.inference_mode():
         if big or tokens >= 1_000_000:
-            run = lambda: model(x)  # noqa: E731  (launch-overhead-free at this size)
+            run = lambda: model(x, mask)  # noqa: E731  (launch-overhead-free at this size)
             mode = "eager"
         else:
             # The reference harness's choice (cuda_graph_runner.maybe_cuda_graph):
             # replay with the output clone, or eager for a one-kernel forward.
-            runner, graphed, status = graphs.maybe_cuda_graph(model, x, None, enabled=True)
-            run = lambda: runner(x)  # noqa: E731
+            runner, graphed, status = graphs.maybe_cuda_graph(model, x, mask, enabled=True)
+            run = lambda: runner(x, mask)  # noqa: E731
             mode = "hipGraph replay" if graphed else f"eager: {status}"
         if big or (is_head and args.rounds == 1):
             ms, wall = time_steps(run, steps, warmup)
@@ -638,10 +706,16 @@ def run_config(args, pkg, config, shape_id, name, is_head, build, make_input, ti
             n_rounds = args.rounds if is_head else 3
             rounds = [time_steps(run, steps, warmup if r == 0 else 0) for r in range(n_rounds)]
             ms, wall = statistics.median(r[0] for r in rounds), sum(r[1] for r in rounds)
-        out = model(x)
+        ref_stats = None
+        if not args.profile_only:
+            ref_stats = reference_timing(run, 2 if big else args.ref_repeats, 1 if big else args.ref_rounds)
+        out = model(x, mask)
         torch.cuda.synchronize()
     entry_ = {"workload": name, "official_shape": shape_id, "status": "PASS", "tokens_per_s": tokens / (ms / 1e3),
-              "ms": ms, "mode": mode, "steps": steps, "plan": plan.describe()}
+              "ms": ms, "mode": mode, "steps": steps, "plan": plan.describe(),
+              "timed_call": "forward(x, valid_token_mask=all True) as the reference harness (TTB:1478-1491)"}
+    if ref_stats is not None:
+        entry_["reference_harness_timing"] = ref_stats
     flops = pkg.forward_flops(config)
     bound, t_bound = forward_lower_bound(config, flops)
     entry_["forward_roofline"] = {"bound": bound, "frac": t_bound / (ms / 1e3),
@@ -653,10 +727,11 @@ def run_config(args, pkg, config, shape_id, name, is_head, build, make_input, ti
     head_extra = {}
     if not args.profile_only:
         reps = 1 if big else max(2, min(steps, 5))
-        per, dominant = kernel_profile(model, x, config, tokens, reps, lead=0 if big else 20)
+        per, dominant = kernel_profile(model, x, mask, config, tokens, reps, ms, lead=0 if big else 20)
         k = per[dominant]
         entry_["roofline"] = {"kernel": dominant, "bound": k["bound"], "achieved": k["achieved"], "peak": k["peak"],
                               "unit": k["unit"], "frac": k["frac"], "avg_us": k["avg_ms"] * 1e3,
+                              "time_source": k["time_source"],
                               "share_of_step": k["share_ms"] / ms, "bytes_per_launch": k["bytes_per_launch"],
                               "flops_per_launch": k["flops_per_launch"]}
         entry_["kernels"] = {n: {"avg_us": round(v["avg_ms"] * 1e3, 2), "per_step": v["launches_per_step"],
@@ -665,31 +740,43 @@ def run_config(args, pkg, config, shape_id, name, is_head, build, make_input, ti
         for kname, v in sorted(per.items(), key=lambda kv: -kv[1]["share_ms"]):
             log(f"[bench]   {kname:28s} {v['avg_ms'] * 1e3:9.1f} us x{v['launches_per_step']} "
                 f"{v['achieved']:9.1f} {v['unit']} ({v['frac'] * 100:5.1f}% {v['bound']})")
+    # Device memory of the timed forward (streamed_shape14.py:174-175): model,
+    # input, mask, the forward's working set and the replay's output clone.
+    entry_["peak_memory"] = {"allocated_gib": torch.cuda.max_memory_allocated(device) / 2**30,
+                             "reserved_gib": torch.cuda.max_memory_reserved(device) / 2**30,
+                             "estimate_gib": device_estimate_bytes(pkg, config) / 2**30}
     log(f"[bench] {name}: {ms:.3f} ms/step, {entry_['tokens_per_s']:.4g} tokens/s ({mode}); plan {plan.describe()}; "
         f"forward {entry_['forward_roofline']['frac']:.3f} of its {bound} lower bound"
         + (f"; dominant {entry_['roofline']['kernel']} at {entry_['roofline']['frac']:.3f} of "
-           f"{entry_['roofline']['bound']} peak" if "roofline" in entry_ else ""))
+           f"{entry_['roofline']['bound']} peak" if "roofline" in entry_ else "")
+        + (f"; reference harness median {ref_stats['median_ms']:.4f} ms" if ref_stats else "")
+        + f"; peak allocated {entry_['peak_memory']['allocated_gib']:.2f} GiB")
 
     if not args.profile_only:
         bad = nonfinite_count(out)
         rows = accuracy_rows(config, args.full_accuracy)
         checks = check_rows(baseline, config, out, x, rows)
-        if is_head:
-            checks += extra_trials(baseline, model, config, min(config.batch_size, sample_rows(shape_id, config)),
-                                   args.accuracy_trials)
-        passed = all(c.passed for c in checks) and bad == 0
+        del out
+        small = not big and tokens < 1_000_000
+        trials = args.accuracy_trials if small else min(args.accuracy_trials, 2)
+        t_rows = trial_rows(config)
+        checks += seeded_trials(baseline, model, config, trials, t_rows)
+        handoff = kernels.split_handoff_failures(device) - failures_before
+        passed = all(c.passed for c in checks) and bad == 0 and handoff == 0
         entry_["accuracy"] = {
             "passed": passed, "failed": sum(c.failed_elements for c in checks),
             "total": sum(c.total_elements for c in checks), "max_abs": max(c.max_abs_error for c in checks),
-            "sequences_checked": len(rows), "trials": 1 + (args.accuracy_trials - 1 if is_head else 0),
-            "nonfinite_in_whole_output": bad,
+            "timed_input_sequences_checked": len(rows),
+            "trials": 1 + trials, "seeded_trials": trials, "trial_seeds": f"1234+t, t < {trials}",
+            "trial_sequences_checked": len(t_rows),
+            "nonfinite_in_whole_output": bad, "split_handoff_failures": handoff,
             "prefix": LONG_PREFIX if config.seq_len > 8192 else None,
         }
         if not passed:
             entry_["status"] = "FAIL"
-        log(f"[bench] {name}: accuracy on {len(rows)} sequences: failed {entry_['accuracy']['failed']}/"
-            f"{entry_['accuracy']['total']}, max_abs {entry_['accuracy']['max_abs']:.3g}; non-finite in the whole "
-            f"output: {bad}")
+        log(f"[bench] {name}: accuracy: timed input on {len(rows)} sequences + {trials} seeded trials on "
+            f"{len(t_rows)}: failed {entry_['accuracy']['failed']}/{entry_['accuracy']['total']}, max_abs "
+            f"{entry_['accuracy']['max_abs']:.3g}; non-finite in the whole output: {bad}; failed hand-offs: {handoff}")
         if not args.no_cpu_baseline or is_head:
             budget = 0.0 if args.no_cpu_baseline else (args.cpu_seconds if is_head else min(args.cpu_seconds, 5.0))
             cpu = cpu_leg(baseline, config, x, budget, sample_rows(shape_id, config))
@@ -698,18 +785,20 @@ def run_config(args, pkg, config, shape_id, name, is_head, build, make_input, ti
                 f"({cpu['sample']})")
             if is_head:
                 head_extra["cpu_baseline"] = cpu
+    else:
+        del out
     if shape_id == 6 and not args.profile_only and not args.batch:
         # The reference's own shape-6 form: chunks of 1024 with a hipGraph per chunk shape.
         chunked = chunking.BatchChunkedTransformer(model, 1024, all_tokens_valid=True, use_cuda_graphs=True)
         with torch.inference_mode():
             c_ms, _ = time_steps(lambda: chunked(x), 10, 2)
-            same = bool(torch.equal(chunked(x), out))
+            same = bool(torch.equal(chunked(x), model(x, mask)))
         entry_["reference_form_chunk1024_graphs"] = {
             "ms": c_ms, "tokens_per_s": tokens / (c_ms / 1e3), "equal_to_unchunked": same,
             "status": chunked.graph_status}
         log(f"[bench] {name}: chunk-1024 per-chunk graphs {c_ms:.3f} ms ({chunked.graph_status}); bitwise equal: {same}")
         del chunked
-    del baseline, model, x, out
+    del baseline, model, x
     return entry_, head_extra
 
 

@@ -929,11 +929,22 @@ struct DecodeGeometry {
   int64_t o_bytes, bytes;  // partial o, then (offset, sum) pairs
 };
 
+// Bytes of one split's partials for one (batch, head): kDecodeQueries rows of
+// HD FP32 outputs plus an (offset, sum) pair each.
+static int64_t decode_split_bytes(int HD) {
+  return (int64_t)kDecodeQueries * (HD * (int64_t)sizeof(float) + (int64_t)sizeof(float2));
+}
+
+// The split count is also capped so that the partials fit the no-allocation
+// entry point's static scratch whenever one split per (batch, head) does:
+// both entry points then run the same geometry and give the same bits.
 static DecodeGeometry decode_geometry(int B, int H, int S_k, int HD) {
   const int bk = HD >= 256 ? 32 : 64;
   const int tiles = (S_k + bk - 1) / bk;
   const int64_t bh = (int64_t)B * H;
-  const int64_t want = std::min<int64_t>(tiles, std::max<int64_t>(1, (kDecodeTargetBlocks + bh - 1) / bh));
+  const int64_t fit = std::max<int64_t>(1, XB_DECODE_SCRATCH_BYTES / (bh * decode_split_bytes(HD)));
+  const int64_t want = std::min<int64_t>(std::min<int64_t>(tiles, fit),
+                                         std::max<int64_t>(1, (kDecodeTargetBlocks + bh - 1) / bh));
   const int tiles_per = (int)((tiles + want - 1) / want);
   DecodeGeometry g;
   g.split_keys = tiles_per * bk;

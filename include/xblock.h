@@ -246,10 +246,18 @@ int xb_attention_kv_cache(const void* qkv, const void* k_cache,
  * forbid hipMalloc).  No counterpart in the reference.  A decode chunk's
  * split partials go to a static device buffer of XB_DECODE_SCRATCH_BYTES
  * that the library holds on each GPU it runs on until the process ends; the
- * call allocates nothing.  A call needing more than that (batch * heads
- * beyond about 7,900 at head_dim 64, 2,000 at head_dim 256) returns
+ * call allocates nothing.  The partials take
+ *   batch * heads * n_splits * 16 * (4 * head_dim + 8) bytes,
+ * and the split count n_splits (>= 1; the same in both entry points, which
+ * is what keeps their results equal) is capped so that this stays within
+ * XB_DECODE_SCRATCH_BYTES whenever n_splits = 1 does.  So a decode chunk
+ * (at most 16 new tokens) fails only when batch * heads * 16 *
+ * (4 * head_dim + 8) > XB_DECODE_SCRATCH_BYTES, whatever the cache length:
+ * batch * heads above 52,428 / 29,127 / 15,420 / 7,943 / 4,032 / 2,032 at
+ * head_dim 8 / 16 / 32 / 64 / 128 / 256.  Such a call returns
  * XB_ERR_SCRATCH_TOO_SMALL without launching; use xb_attention_kv_cache with
- * a workspace then.  The stream must belong to the current device
+ * a workspace then (xb_attention_kv_cache_workspace_bytes gives the bytes
+ * either call needs).  The stream must belong to the current device
  * (XB_ERR_WRONG_DEVICE otherwise).  All calls on one GPU share its buffer:
  * calls that overlap in time on one GPU (different streams, or concurrent
  * graph replays) race and must not be issued.  Results equal

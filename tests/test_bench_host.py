@@ -56,3 +56,15 @@ def test_kernel_costs_match_the_formulas(pkg):
     _, fused_flops = bench.kernel_costs("fused_forward_d128", cfg2, m2)
     assert fused_flops == pytest.approx(pkg.forward_flops(cfg2))
     assert bench.kernel_costs("kv_append_hd64", cfg2, m2) == (0.0, 0.0)
+
+
+def test_trial_rows_follow_the_reference_trials(pkg):
+    shapes = pkg.OFFICIAL_BENCHMARK_SHAPES
+    for shape_id in (1, 8, 11):                       # small configs: every sequence of each trial
+        assert bench.trial_rows(shapes[shape_id]) == list(range(shapes[shape_id].batch_size))
+    rows = bench.trial_rows(shapes[6])                # cfg2: 1024 sequences from the start, middle and end
+    assert len(rows) == 1024 and rows == sorted(set(rows)) and rows[0] == 0 and rows[-1] == 9999
+    assert 5000 in rows
+    assert bench.trial_rows(shapes[14]) == [0, 16, 31]
+    args = bench.parse_args([])
+    assert args.accuracy_trials == 5 and args.ref_repeats == 100 and args.ref_rounds == 3   # TTB:1618-1623

@@ -187,6 +187,34 @@ def test_library_exports_every_declared_symbol(capi):
     assert capi.lib().xb_abi_version() == capi.XB_ABI_VERSION
 
 
+SCRATCH_BYTES = 32 << 20   # XB_DECODE_SCRATCH_BYTES
+
+
+def _check_noalloc_scratch_rule(lib):
+    """The no-allocation decode's documented limit, from the library's own sizing.
+
+    A decode chunk's partials (batch*heads*n_splits*16*(4*head_dim+8) bytes)
+    fit the static scratch whenever one split per (batch, head) does, at any
+    cache length; beyond that the call is refused (-9) before any launch.
+    Only the refusals are called here: an accepted call would launch.
+    """
+    limits = {8: 52428, 16: 29127, 32: 15420, 64: 7943, 128: 4032, 256: 2032}
+    for head_dim, limit in limits.items():
+        assert limit == SCRATCH_BYTES // (16 * (4 * head_dim + 8))
+        for bh in (1, 13, 16, 33, 48, 512, 2000, limit):
+            for cached in (31, 4000, 100000):
+                need = lib.xb_attention_kv_cache_workspace_bytes(bh, 1, 1, head_dim, cached)
+                assert 0 < need <= SCRATCH_BYTES, (head_dim, bh, cached, need)
+        for cached in (31, 100000):
+            need = lib.xb_attention_kv_cache_workspace_bytes(limit + 1, 1, 1, head_dim, cached)
+            assert need == (limit + 1) * 16 * (4 * head_dim + 8) > SCRATCH_BYTES
+            assert lib.xb_attention_kv_cache_noalloc(16, 16, 16, 16, limit + 1, 1, 1, head_dim, cached,
+                                                     cached + 1, 0.1, None) == -9
+    # the long caches still split over many key ranges (a workspace call and
+    # a no-allocation call share this geometry)
+    assert lib.xb_attention_kv_cache_workspace_bytes(1, 1, 16, 256, 100000) > 100 * 16 * 16 * 1032
+
+
 def test_argument_errors_need_no_gpu(capi):
     lib = capi.lib()
     assert lib.xb_linear(None, None, None, None, 4, 8, 8, 0, None) == -1
@@ -242,6 +270,7 @@ def test_argument_errors_need_no_gpu(capi):
     assert lib.xb_attention_kv_cache_noalloc(16, 16, 16, 16, 20000, 1, 16, 64, 100, 101, 0.1, None) == -9
     assert lib.xb_attention_kv_cache_noalloc(None, 16, 16, 16, 1, 1, 2, 64, 100, 101, 0.1, None) == -1
     assert lib.xb_attention_kv_cache_noalloc(16, 16, 16, 16, 1, 1, 2, 64, 100, 100, 0.1, None) == -2
+    _check_noalloc_scratch_rule(lib)
     for code in (0, -1, -2, -3, -4, -5, -6, -7, -8, -9):
         assert lib.xb_strerror(code)
     with pytest.raises(RuntimeError, match="xb_linear failed with code -4"):

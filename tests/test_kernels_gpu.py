@@ -202,6 +202,74 @@ def test_attention_long_hd64_ping_pong(pkg, cuda, b, s, h, causal):
     assert torch.equal(out, pkg.attention(qg, h, key_valid=ones, causal=causal))
 
 
+def _rows_reference(qkv: torch.Tensor, heads: int, rows) -> torch.Tensor:
+    """FP32 causal attention of the given query rows of one sequence ([1, S, 3D] FP16):
+    O(S * head_dim) per row, so any row of a 100,000-token sequence is cheap."""
+    _, s, width = qkv.shape
+    d = width // 3
+    hd = d // heads
+    t = qkv[0].float().view(s, 3, heads, hd)
+    q, k, v = t[:, 0].transpose(0, 1), t[:, 1].transpose(0, 1), t[:, 2].transpose(0, 1)   # [H, S, hd]
+    idx = torch.tensor(rows)
+    scores = (q[:, idx] @ k.transpose(1, 2)) * hd**-0.5                                    # [H, R, S]
+    scores = scores.masked_fill(torch.arange(s)[None, None, :] > idx[None, :, None], float("-inf"))
+    return (torch.softmax(scores, -1) @ v).transpose(0, 1).reshape(len(rows), d)
+
+
+def test_attention_full_length_cfg5_sampled_rows(pkg, cuda):
+    """cfg5's attention at its real length (S = 100,000, head_dim 64) beyond
+    the 4096-token prefix the model tests check: the ping-pong kernel over
+    the packed projection, the V-transposed form the cfg5 model runs (fed by
+    xb_linear_qkv_vt through an identity projection, so its input is exactly
+    the same projection), and the four-wave kernel under an all-valid key
+    mask are bitwise equal over the whole output, and sampled query rows
+    match an FP32 reference computed on the CPU from the same FP16 values.
+
+    The rows sampled: the first and last ones, rows on 64-key tile and
+    512-query block edges through the sequence, and the rows at and after two
+    planted keys whose scores with every later query (about 16 and 26)
+    exceed everything before them by about 10 (natural log), so the online
+    softmax must move its running offset and rescale the partial output at
+    positions 60,001 and 99,000 (offsets move lazily, only past a margin)."""
+    capi = pkg._capi
+    b, s, h, hd = 1, 100000, 2, 64
+    d = h * hd
+    g = _gen(100000)
+    qkv = torch.randn(b, s, 3 * d, generator=g)
+    q = qkv[..., :d].view(s, h, hd)
+    q += 1.0                                       # every query leans on the all-ones direction
+    planted = {60001: 2.0, 99000: 3.25}            # key position -> multiple of the all-ones vector
+    k = qkv[..., d:2 * d].view(s, h, hd)
+    for pos, alpha in planted.items():
+        k[pos] = alpha                             # score ~ alpha * 64 / 8 with every later query
+    qkv = qkv.half()
+    rows = sorted({0, 1, 63, 64, 511, 512, 513, 4095, 4096, 4097, 50175, 50176, 60000, 60001, 60002, 60063,
+                   60064, 60543, 60544, 61000, 98999, 99000, 99001, 99455, 99456, 99967, 99968, 99998, 99999}
+                  | set(torch.randint(0, s, (16,), generator=g).tolist()))
+    ref = _rows_reference(qkv, h, rows)
+    qg = qkv.to(cuda)
+    print(f"attention S={s} hd={hd} heads={h}: {len(rows)} sampled rows", flush=True)
+    out = pkg.attention(qg, h, causal=True, variant=capi.XB_ATTN_PINGPONG)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all())
+    got = out[0, rows].cpu().float()
+    torch.testing.assert_close(got, ref, atol=2e-3, rtol=1e-2)
+    # the planted keys dominate the rows after them: the offset did have to move
+    late = torch.tensor([r >= 60001 for r in rows])
+    v_planted = qkv[0, 60001, 2 * d:].float()
+    assert float((ref[late & torch.tensor([r < 99000 for r in rows])] - v_planted).abs().mean()) < 0.1
+    ones = torch.ones(b, s, dtype=torch.bool, device=cuda)
+    assert torch.equal(out, pkg.attention(qg, h, key_valid=ones, causal=True)), "four-wave kernel differs"
+    # The V-transposed form: an identity projection (K = 3D = 384) reproduces qkv exactly.
+    eye = torch.eye(3 * d, dtype=torch.float16, device=cuda)
+    zero = torch.zeros(3 * d, device=cuda)
+    assert torch.equal(pkg.linear(qg, eye, zero), qg)
+    qkv_vt, vt = pkg.linear_qkv_vt(qg, eye, zero, h)
+    out_vt = pkg.attention_vt(qkv_vt, vt, h)
+    torch.cuda.synchronize()
+    assert torch.equal(out_vt, out), "V-transposed form differs from the ping-pong kernel"
+
+
 def _key_order(s):
     """Position of each token of a row of the transposed V: inside every
     32-token group, token 32t + 4g + i sits at 32t + 8g + i and token

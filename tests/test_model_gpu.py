@@ -556,6 +556,7 @@ def test_fused_split_graph_replay_and_smaller_batch(pkg, cuda):
     args = dict(num_heads=4, ffn_dim=128, num_layers=2, affine_mask=affine)
     xg = torch.randn(16, 128, 128, generator=torch.Generator().manual_seed(71)).to(cuda)
     timeouts = kernels.fused_split_timeouts(cuda)
+    failures = kernels.split_handoff_failures(cuda)
     with torch.inference_mode():
         eager = kernels.fused_forward_d128(xg, wpack, ppack, split=False, **args)
         out = torch.empty_like(xg)
@@ -570,8 +571,6 @@ def test_fused_split_graph_replay_and_smaller_batch(pkg, cuda):
         graph = torch.cuda.CUDAGraph()
         with pool, torch.cuda.graph(graph, stream=side):
             kernels.fused_forward_d128(xg, wpack, ppack, out=out, **args)
-        # outside any pool, a capture takes no workspace (one-workgroup form)
-        assert kernels.fused_split_workspace(cuda, 16, 128, 4, 2, True) is not None
         launches = kernels.split_launches_of(ws)
         for replay in range(3):
             out.zero_()
@@ -589,6 +588,28 @@ def test_fused_split_graph_replay_and_smaller_batch(pkg, cuda):
         torch.cuda.synchronize()
         assert torch.equal(out, eager), "replay after the smaller batch"
         assert kernels.fused_split_timeouts(cuda) == timeouts and pool.timeouts() == 0
+
+        # A capture outside any pool takes no workspace: it records the
+        # one-workgroup form, so its replays give the same result and leave
+        # every eager workspace (the side stream's and the current one's) alone.
+        plain_out = torch.empty_like(xg)
+        with torch.cuda.stream(side):
+            kernels.fused_forward_d128(xg, wpack, ppack, out=plain_out, **args)  # makes the side stream's workspace
+            side_ws = kernels.fused_split_workspace(cuda, 16, 128, 4, 2, True)
+        torch.cuda.synchronize()
+        plain = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(plain, stream=side):
+            assert kernels.fused_split_workspace(cuda, 16, 128, 4, 2, True) is None
+            kernels.fused_forward_d128(xg, wpack, ppack, out=plain_out, **args)
+        eager_ws = [side_ws, kernels.fused_split_workspace(cuda, 16, 128, 4, 2, True)]
+        counts = [kernels.split_launches_of(w) for w in eager_ws]
+        for replay in range(2):
+            plain_out.zero_()
+            plain.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(plain_out, eager), f"pool-less replay {replay}"
+        assert [kernels.split_launches_of(w) for w in eager_ws] == counts, "a pool-less replay used an eager workspace"
+        assert kernels.split_handoff_failures(cuda) == failures
 
 
 @pytest.mark.parametrize("fault", ["no_publish", "foreign_xcd"])

@@ -73,6 +73,12 @@ def test_maybe_cuda_graph_reasons(pkg, cuda):
     assert graphs.maybe_cuda_graph(model, x, None, enabled=False)[1:] == (False, "disabled")
     runner, graphed, reason = graphs.maybe_cuda_graph(model, x, None, enabled=True)
     assert runner is model and not graphed and "one-kernel" in reason
+    # the reference harness's all-True mask runs the unmasked one-kernel forward too
+    all_valid = torch.ones(4, 64, dtype=torch.bool, device=cuda)
+    runner, graphed, reason = graphs.maybe_cuda_graph(model, x, all_valid, enabled=True)
+    assert runner is model and not graphed and "one-kernel" in reason
+    with torch.inference_mode():
+        assert torch.equal(model(x, all_valid), model(x))
     model.enable_kv_cache(True)
     assert "KV-cache" in graphs.maybe_cuda_graph(model, x, None, enabled=True)[2]
     model.enable_kv_cache(False)
