@@ -676,19 +676,20 @@ __device__ __forceinline__ void split_layer_norm2(const float4_t (&res)[NBT][OB]
     for (int j = 0; j < OK; ++j) {
       const int ks = OK * half + j;
       float4_t lo, hi;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        lo[i] = fmaf(res[b][2 * j][i], rstd[b], shift);
+        hi[i] = fmaf(res[b][2 * j + 1][i], rstd[b], shift);
+      }
+      // The affine step updates lo / hi in place, so both branches leave the
+      // values in the same registers (no copies at the join).
       if (affine) {
         const float4_t g0 = ld4(gamma + 32 * ks + 4 * g), g1 = ld4(gamma + 32 * ks + 16 + 4 * g);
         const float4_t b0 = ld4(beta + 32 * ks + 4 * g), b1 = ld4(beta + 32 * ks + 16 + 4 * g);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          lo[i] = fmaf(fmaf(res[b][2 * j][i], rstd[b], shift), g0[i], b0[i]);
-          hi[i] = fmaf(fmaf(res[b][2 * j + 1][i], rstd[b], shift), g1[i], b1[i]);
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          lo[i] = fmaf(res[b][2 * j][i], rstd[b], shift);
-          hi[i] = fmaf(res[b][2 * j + 1][i], rstd[b], shift);
+          lo[i] = fmaf(lo[i], g0[i], b0[i]);
+          hi[i] = fmaf(hi[i], g1[i], b1[i]);
         }
       }
       own[b][j] = to_operand(lo, hi);
