@@ -700,6 +700,9 @@ def run_config(args, pkg, config, shape_id, name, is_head, build, make_input, ti
             runner, graphed, status = graphs.maybe_cuda_graph(model, x, mask, enabled=True)
             run = lambda: runner(x, mask)  # noqa: E731
             mode = "hipGraph replay" if graphed else f"eager: {status}"
+            overlap = model.captured_overlap(config.batch_size, config.seq_len) if graphed else None
+            if overlap:
+                mode += f"; {overlap}"
         if big or (is_head and args.rounds == 1):
             ms, wall = time_steps(run, steps, warmup)
         else:

@@ -39,6 +39,7 @@ reference (TTB:503-508) there is no sequence-length limit: the key mask is a
 
 from __future__ import annotations
 
+import dataclasses
 from typing import Dict, Optional, Tuple
 
 import torch
@@ -442,11 +443,86 @@ class UserOptimizedTransformer(nn.Module):
                                               split=plan.fused_variant == _capi.XB_FUSED_SPLIT,
                                               strict=self._strict_handoff_checks)
 
-        def attend(index: int, layer: TransformerBlockParameters, qkv: torch.Tensor) -> torch.Tensor:
-            return kernels.attention(qkv, cfg.num_heads, key_valid=token_valid, causal=cfg.causal,
-                                     scale=layer.attention.scale, variant=plan.attention_variant)
+        def attend_with(key_valid: Optional[torch.Tensor]):
+            def attend(index: int, layer: TransformerBlockParameters, qkv: torch.Tensor) -> torch.Tensor:
+                return kernels.attention(qkv, cfg.num_heads, key_valid=key_valid, causal=cfg.causal,
+                                         scale=layer.attention.scale, variant=plan.attention_variant)
+            return attend
 
-        return self._per_op_forward(x, attend, plan, out=out, token_valid=token_valid)
+        streams = self._overlap_streams(x)
+        if streams is not None and torch.cuda.is_current_stream_capturing():
+            return self._per_op_forward_overlapped(x, attend_with, plan, streams, out, token_valid)
+        return self._per_op_forward(x, attend_with(token_valid), plan, out=out, token_valid=token_valid)
+
+    # A small per-op forward captured into a hipGraph runs as two half-batches
+    # on two streams forked from the capturing stream and joined back into it.
+    # Each half takes the GEMM tiles the plan picks for its own row count for
+    # the output projection and the FFN (128 x 128 at 4096 rows: 256 tiles,
+    # every CU, instead of 128 x 256 tiles that leave half of them idle at
+    # that size), so the two halves' single-round grids run side by side and
+    # fill each other's ramp-up and drain; the QKV projection and the
+    # attention keep the whole batch's variants.  Every direct-to-LDS tile
+    # gives the same bits, and batch elements are independent, so the rows
+    # equal the whole batch's bit for bit.  Measured under graph replay, in
+    # one call: cfg3 725.8 -> 681.3 us; D = 1024 with 16 heads of 64 at the
+    # same size 730.5 -> 694.9 us.  With both halves on the whole batch's
+    # tiles the overlap gained nothing (734.7 us), and four streams no more
+    # than two.  Eager calls stay on one stream: there the host's per-launch
+    # cost, paid twice, outweighs it.
+    _OVERLAP_MAX_TOKENS = 32768
+
+    def _overlap_streams(self, x: torch.Tensor) -> Optional[Tuple[torch.cuda.Stream, torch.cuda.Stream]]:
+        """The two side streams of x's device for an overlapped capture, or None when x does not qualify.
+
+        Made on the first qualifying call outside capture (the eager warm-up
+        calls before a capture are such calls), at the default priority.
+        """
+        if x.shape[0] < 2 or x.shape[0] * x.shape[1] > self._OVERLAP_MAX_TOKENS:
+            return None
+        per_device = self.__dict__.setdefault("_side_streams", {})
+        streams = per_device.get(x.device.index)
+        if streams is None and not torch.cuda.is_current_stream_capturing():
+            streams = (torch.cuda.Stream(device=x.device), torch.cuda.Stream(device=x.device))
+            per_device[x.device.index] = streams
+        return streams
+
+    def captured_overlap(self, batch: int, seq_len: int, padded: bool = False) -> Optional[str]:
+        """What a forward of [batch, seq_len] captured into a hipGraph runs beyond its plan, or None.
+
+        A captured small per-op forward runs as two half-batches on two
+        streams, each with its own GEMM tiles for the output projection and
+        the FFN (see _OVERLAP_MAX_TOKENS); this names them.
+        """
+        plan = self.execution_plan(batch, seq_len, padded=padded)
+        if plan.fused or batch < 2 or batch * seq_len > self._OVERLAP_MAX_TOKENS or self._kv_cache_enabled:
+            return None
+        halves = sorted({(batch + 1) // 2, batch // 2}, reverse=True)
+        own = [self.execution_plan(h, seq_len, padded=padded, per_op=True) for h in halves]
+        names = ", ".join(f"{h} sequences: out {p.projection_strategy.split('out ')[-1]}, FFN {p.ffn_strategy}"
+                          for h, p in zip(halves, own))
+        return f"two half-batch streams under capture ({names}); QKV and attention as planned"
+
+    def _per_op_forward_overlapped(self, x: torch.Tensor, attend_with, plan: ShapeExecutionPlan,
+                                   streams: Tuple[torch.cuda.Stream, torch.cuda.Stream],
+                                   out: Optional[torch.Tensor], token_valid: Optional[torch.Tensor]) -> torch.Tensor:
+        """_per_op_forward of each half of the batch on its own stream, joined back into the current one."""
+        batch, seq_len = x.shape[0], x.shape[1]
+        if out is None:
+            out = torch.empty_like(x)
+        main = torch.cuda.current_stream(x.device)
+        half = (batch + 1) // 2
+        for stream, (start, end) in zip(streams, ((0, half), (half, batch))):
+            valid = None if token_valid is None else token_valid[start:end]
+            own = self.execution_plan(end - start, seq_len, padded=token_valid is not None, per_op=True)
+            half_plan = dataclasses.replace(plan, out_variant=own.out_variant, ffn_in_variant=own.ffn_in_variant,
+                                            ffn_out_variant=own.ffn_out_variant)
+            stream.wait_stream(main)
+            with torch.cuda.stream(stream):
+                self._per_op_forward(x[start:end], attend_with(valid), half_plan, out=out[start:end],
+                                     token_valid=valid)
+        for stream in streams:
+            main.wait_stream(stream)
+        return out
 
     def _forward_hip_cached(self, x: torch.Tensor) -> torch.Tensor:
         """One KV-cached step: append this chunk's keys/values per layer, attend over the cache.

@@ -275,3 +275,20 @@ def test_argument_errors_need_no_gpu(capi):
         assert lib.xb_strerror(code)
     with pytest.raises(RuntimeError, match="xb_linear failed with code -4"):
         capi.check(-4, "xb_linear")
+
+
+def test_captured_overlap_is_described(pkg):
+    """The plan of a small per-op forward names what its hipGraph capture runs
+    (two half-batches, each with its own out / FFN GEMM tiles); one-kernel,
+    large and single-sequence forwards run as planned."""
+    shapes = pkg.OFFICIAL_BENCHMARK_SHAPES
+    cfg3 = pkg.UserOptimizedTransformer(shapes[8])
+    note = cfg3.captured_overlap(64, 128)
+    assert note.startswith("two half-batch streams under capture (32 sequences: out mfma_gemm_dma_128x128")
+    assert cfg3.captured_overlap(1, 128) is None                                  # nothing to split
+    assert cfg3.captured_overlap(512, 128) is None                                # 65536 tokens: long kernels
+    for shape_id in (1, 6, 11):                                                   # one-kernel whole-stack forwards
+        c = shapes[shape_id]
+        assert pkg.UserOptimizedTransformer(c).captured_overlap(c.batch_size, c.seq_len) is None
+    odd = pkg.UserOptimizedTransformer(pkg.TransformerConfig(7, 64, 1024, 4, 1024, 1, True))
+    assert "4 sequences" in odd.captured_overlap(7, 64, padded=True) and "3 sequences" in odd.captured_overlap(7, 64)

@@ -636,9 +636,11 @@ def test_fused_split_timeout_poisons_rows(pkg, cuda, geom, fault):
     with torch.inference_mode():
         one = kernels.fused_forward_d128(xg, wpack, ppack, split=False, **args)
         before = kernels.fused_split_timeouts(cuda)
+        before_all = kernels.split_handoff_failures(cuda)
         bad = kernels.fused_forward_d128(xg, wpack, ppack, **forced, **args)
         torch.cuda.synchronize()
         assert kernels.fused_split_timeouts(cuda) - before == b * layers
+        assert kernels.split_handoff_failures(cuda) - before_all == b * layers  # the process-wide count sees them
         assert bool(torch.isnan(bad[:, 64:]).all()), "rows of the waiting workgroups must be NaN"
         assert torch.equal(bad[:, :64], one[:, :64]), "rows of the first workgroups are unaffected"
         good = kernels.fused_forward_d128(xg, wpack, ppack, strict=True, **args)

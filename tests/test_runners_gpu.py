@@ -92,6 +92,56 @@ def test_maybe_cuda_graph_reasons(pkg, cuda):
         assert torch.equal(runner(x, mask), model(x, mask))
 
 
+@pytest.mark.parametrize("geom,masked", [((5, 96, 256, 4, 512, 2), False), ((7, 64, 1024, 4, 1024, 1), True),
+                                         ((2, 4096, 1024, 16, 1024, 1), False)])
+def test_captured_per_op_forward_overlaps_half_batches(pkg, cuda, geom, masked):
+    """A small per-op forward captured into a graph runs its two half-batches
+    (odd batches: 3 + 2 and 4 + 3 sequences) on two side streams forked from
+    the capturing stream; the replays equal the eager one-stream forward bit
+    for bit, padded mask included, with eager forwards between them.  The
+    side streams are made by the eager warm-up calls before the capture.
+    The last geometry (8192 tokens of the long-sequence kind) checks the
+    transposed-V attention inside the overlap."""
+    graphs, _, _ = _runners(pkg)
+    config = pkg.TransformerConfig(*geom, True)
+    _, model = _models(pkg, config, cuda)
+    g = torch.Generator(device=cuda).manual_seed(11)
+    x = torch.randn(config.batch_size, config.seq_len, config.d_model, generator=g, device=cuda)
+    mask = None
+    if masked:
+        mask = torch.ones(config.batch_size, config.seq_len, dtype=torch.bool, device=cuda)
+        mask[1, 40:] = False
+        mask[5, 3:] = False
+    assert not model.execution_plan(config.batch_size, config.seq_len, padded=masked).fused
+    with torch.inference_mode():
+        eager = model(x, mask).clone()
+    graphed = graphs.FixedInputCUDAGraph(model, x, mask)
+    assert cuda.index in model.__dict__.get("_side_streams", {}), "the warm-up calls make the side streams"
+    with torch.inference_mode():
+        for replay in range(3):
+            out = graphed(x, mask)
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager), f"{geom} masked={masked} replay {replay}"
+            assert torch.equal(model(x, mask), eager)
+
+
+def test_maybe_cuda_graph_refuses_a_failed_handoff(pkg, cuda, monkeypatch):
+    """A graph whose check run counted a failed split-form K/V hand-off (its
+    rows would be NaN) is refused with the cause named, and the forward stays
+    eager.  The failure count is faked from the host (a real failure is
+    forced in test_fused_split_timeout_poisons_rows); every kernel runs
+    normally."""
+    graphs, _, kernels = _runners(pkg)
+    config = pkg.TransformerConfig(2, 64, 256, 4, 512, 2, True)   # per-op forward: captured
+    _, model = _models(pkg, config, cuda)
+    x = torch.randn(2, 64, 256, device=cuda)
+    counts = iter((0, 3))
+    monkeypatch.setattr(kernels, "split_handoff_failures", lambda device=None: next(counts))
+    runner, graphed, reason = graphs.maybe_cuda_graph(model, x, None, enabled=True)
+    assert runner is model and not graphed
+    assert "3 split-form K/V hand-off(s) failed" in reason
+
+
 def test_batch_chunked_graphs_match_whole_batch(pkg, cuda):
     """Per-chunk-shape graphs (full chunk and remainder) over static buffers, split and
     one-workgroup whole-stack forms, plus a per-op geometry: bitwise equal to the
