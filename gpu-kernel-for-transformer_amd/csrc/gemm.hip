@@ -441,14 +441,20 @@ static bool linear_variant_fits(int variant, int64_t m, int n, int k) {
 // CU, so the cost is taken as rounds of 256 tiles x tile area, the 256 x 256
 // tile ~15% cheaper per output (fewer LDS bytes per MFMA); 256 x 192 sits
 // between them and fills whole rounds where 256 x 256 leaves half a round
-// idle (M = 8192, N = 3072: 63 vs 70 us).
+// idle (M = 8192, N = 3072: 54 vs 60 us).  With the banded tile order a
+// 128 x 128 round on an XCD reads about 3 MB of distinct operands at N =
+// 1024, inside its 4 MB L2, and costs ~5% less per output than 128 x 256:
+// a sweep (us, 256x256 / 128x256 / 128x128) of 8192 x 1024 x 1024 gave
+// 31.4 / 22.5 / 21.2, 16384 x 1024 35.4 / 40.9 / 39.6, 3.2M x 1024
+// 7311 / 8542 / 8052, and the factors below reproduce every best choice of
+// that sweep (also 4096 x 1024, 4096 / 8192 / 3.2M x 3072).
 static int select_linear(int64_t m, int n, int k) {
   auto tiles = [&](int64_t bm, int64_t bn) { return ((m + bm - 1) / bm) * ((n + bn - 1) / bn); };
   if (k % 64 == 0 && k >= 256) {
     const int64_t big = (tiles(256, 256) + 255) / 256 * 65536 * 85 / 100;
     const int64_t wide = n % 192 == 0 ? (tiles(256, 192) + 255) / 256 * 49152 * 90 / 100 : INT64_MAX;
     const int64_t mid = (tiles(128, 256) + 255) / 256 * 32768;
-    const int64_t small = (tiles(128, 128) + 255) / 256 * 16384 * 115 / 100;
+    const int64_t small = (tiles(128, 128) + 255) / 256 * 16384 * 95 / 100;
     if (big <= wide && big <= mid && big <= small) return XB_LINEAR_DMA_256x256;
     if (wide <= mid && wide <= small) return XB_LINEAR_DMA_256x192;
     if (mid <= small) return XB_LINEAR_DMA_128x256;
