@@ -42,7 +42,9 @@ leaving idle needs about 30 ms of load before its clock settles: after 2 s
 idle, cfg2's first forwards take 2.6, 2.5, 2.3, 2.2 ms and reach 1.9 ms only
 from the 16th on, so 5 warm-up steps alone leave the ramp inside the timed
 steps.  Then --warmup untimed steps and exactly --steps timed ones, with a
-device synchronisation on both sides.
+device synchronisation on both sides.  The default of 100 timed steps (about
+0.19 s for cfg2) keeps one slow stretch of the clock from moving the
+headline: 20-step windows have read 1.855 and 1.915 ms on one box.
 A config whose device-memory estimate exceeds --memory-fraction of the GPU is
 skipped before anything is allocated, and an out-of-memory error skips it
 (the reference's SAFE_SKIP / SAFE_ABORT, streamed_shape14.py:197-222); for the
@@ -76,8 +78,8 @@ EXIT_ACCURACY = 2                 # torch_transformer_benchmark.py:1862-1865
 def parse_args(argv=None):
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--steps", type=int, default=100)
+    p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--workload", type=int, default=6, choices=range(1, 15), metavar="SHAPE_ID",
                    help="official shape id (1-14) of the headline line; default 6 = BASELINE config 2")
     p.add_argument("--no-per-config", action="store_true", help="skip the other four configs")
@@ -612,6 +614,7 @@ def main(argv=None) -> int:
         "settle_s": args.settle,
         "rounds": args.rounds,
         "ms_per_step": headline["ms"],
+        **({"rounds_ms": headline["rounds_ms"]} if "rounds_ms" in headline else {}),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -703,12 +706,14 @@ def run_config(args, pkg, config, shape_id, name, is_head, build, make_input, ti
             overlap = model.captured_overlap(config.batch_size, config.seq_len) if graphed else None
             if overlap:
                 mode += f"; {overlap}"
+        rounds_ms = None
         if big or (is_head and args.rounds == 1):
             ms, wall = time_steps(run, steps, warmup)
         else:
             n_rounds = args.rounds if is_head else 3
             rounds = [time_steps(run, steps, warmup if r == 0 else 0) for r in range(n_rounds)]
-            ms, wall = statistics.median(r[0] for r in rounds), sum(r[1] for r in rounds)
+            rounds_ms = [r[0] for r in rounds]
+            ms, wall = statistics.median(rounds_ms), sum(r[1] for r in rounds)
         ref_stats = None
         if not args.profile_only:
             ref_stats = reference_timing(run, 2 if big else args.ref_repeats, 1 if big else args.ref_rounds)
@@ -717,6 +722,8 @@ def run_config(args, pkg, config, shape_id, name, is_head, build, make_input, ti
     entry_ = {"workload": name, "official_shape": shape_id, "status": "PASS", "tokens_per_s": tokens / (ms / 1e3),
               "ms": ms, "mode": mode, "steps": steps, "plan": plan.describe(),
               "timed_call": "forward(x, valid_token_mask=all True) as the reference harness (TTB:1478-1491)"}
+    if rounds_ms is not None:
+        entry_["rounds_ms"] = rounds_ms
     if ref_stats is not None:
         entry_["reference_harness_timing"] = ref_stats
     flops = pkg.forward_flops(config)
