@@ -502,57 +502,76 @@ __device__ __forceinline__ void attend16(const half_t* k_lds, const half_t* vt_l
         qh[j] = __builtin_bit_cast(half8_t, w);
       }
     }
-    float4_t sc[LKB + 1];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kb = 0; kb <= LKB; ++kb) {
-      float4_t acc = MODE != 2 && DSTART && kb == QB ? dstart : float4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int j = 0; j < KSH; ++j) {
-        const half8_t kf = *reinterpret_cast<const half8_t*>(k_lds + (16 * kb + r16) * LD + 32 * (ks0 + j) + 8 * g);
-        acc = mfma16x16x32(kf, qh[j], acc);
-      }
-      if (MODE != 2 && !DSTART && kb == QB) {  // -inf above the diagonal: key 4g + i vs query r16
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (4 * g + i > r16) acc[i] = -INFINITY;
-      }
-      if constexpr (MODE != 0) {  // keys 16 kb + 4g .. +3: validity bytes
-        const uint32_t v4 = *reinterpret_cast<const uint32_t*>(kval + 16 * kb + 4 * g);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (((v4 >> (8 * i)) & 0xffu) == 0u) acc[i] = -INFINITY;
-      }
-      sc[kb] = acc;
-      mx = fmaxf(mx, fmaxf(fmaxf(acc[0], acc[1]), fmaxf(acc[2], acc[3])));
-    }
-    mx = quad_group_max(mx);
-    if constexpr (MODE != 0) mx = mx == -INFINITY ? 0.f : mx;  // no visible key: every p is exp2(-inf) = 0
     const half8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
-    float4_t lacc = {0.f, 0.f, 0.f, 0.f};
     const int vrow0 = HD < 16 ? 16 * (h / 2) : h * HD;
-    float4_t o[HDB];
+    float4_t lacc, o[HDB];
+    // The probabilities are exp2 of the raw scores, with no row maximum taken
+    // out: softmax is invariant to that shift, and it is exact arithmetic as
+    // long as the FP16 probabilities neither overflow nor all fall among
+    // FP16's subnormals.  The row sum decides: an overflow makes it infinite,
+    // and a sum >= 1 puts the largest of at most 128 probabilities at >= 2^-7,
+    // so a subnormal one (< 2^-14, absolute error <= 2^-25) is off by at most
+    // 2^-18 of the largest, below FP16's own rounding.  Only when some query
+    // of the wave fails that test does the head run again in the textbook
+    // form, the row maximum subtracted first (and a query that sees no key
+    // at all, sum 0, gets its zero context there).
+    for (bool exact = false;; exact = true) {
+      float4_t sc[LKB + 1];
 #pragma unroll
-    for (int hb = 0; hb < HDB; ++hb) o[hb] = float4_t{0.f, 0.f, 0.f, 0.f};
+      for (int kb = 0; kb <= LKB; ++kb) {
+        float4_t acc = MODE != 2 && DSTART && kb == QB ? dstart : float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kt = 0; kt < NKT; ++kt) {
-      float4_t p0, p1 = {0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < KSH; ++j) {
+          const half8_t kf = *reinterpret_cast<const half8_t*>(k_lds + (16 * kb + r16) * LD + 32 * (ks0 + j) + 8 * g);
+          acc = mfma16x16x32(kf, qh[j], acc);
+        }
+        if (MODE != 2 && !DSTART && kb == QB) {  // -inf above the diagonal: key 4g + i vs query r16
 #pragma unroll
-      for (int i = 0; i < 4; ++i) p0[i] = __builtin_amdgcn_exp2f(sc[2 * kt][i] - mx);
-      if (2 * kt + 1 <= LKB) {  // constant once the loop is unrolled
+          for (int i = 0; i < 4; ++i)
+            if (4 * g + i > r16) acc[i] = -INFINITY;
+        }
+        if constexpr (MODE != 0) {  // keys 16 kb + 4g .. +3: validity bytes
+          const uint32_t v4 = *reinterpret_cast<const uint32_t*>(kval + 16 * kb + 4 * g);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) p1[i] = __builtin_amdgcn_exp2f(sc[2 * kt + 1][i] - mx);
+          for (int i = 0; i < 4; ++i)
+            if (((v4 >> (8 * i)) & 0xffu) == 0u) acc[i] = -INFINITY;
+        }
+        sc[kb] = acc;
       }
-      const half8_t pf = to_operand(p0, p1);
-      lacc = mfma16x16x32(ones, pf, lacc);
+      if (exact) {
+        float mx = -INFINITY;
 #pragma unroll
-      for (int hb = 0; hb < HDB; ++hb) {
-        // V^T columns hold the keys of each 32-key step in the P operand's
-        // order (keys 32kt + 4g + i and 32kt + 16 + 4g + i at 32kt + 8g + i
-        // and + 4): one 16-byte read per fragment.
-        const half8_t vf = *reinterpret_cast<const half8_t*>(vt_lds + (vrow0 + 16 * hb + r16) * LD + 32 * kt + 8 * g);
-        o[hb] = mfma16x16x32(vf, pf, o[hb]);
+        for (int kb = 0; kb <= LKB; ++kb)
+          mx = fmaxf(mx, fmaxf(fmaxf(sc[kb][0], sc[kb][1]), fmaxf(sc[kb][2], sc[kb][3])));
+        mx = quad_group_max(mx);
+        if constexpr (MODE != 0) mx = mx == -INFINITY ? 0.f : mx;  // no visible key: every p is exp2(-inf) = 0
+#pragma unroll
+        for (int kb = 0; kb <= LKB; ++kb) sc[kb] -= mx;
       }
+      lacc = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int hb = 0; hb < HDB; ++hb) o[hb] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kt = 0; kt < NKT; ++kt) {
+        float4_t p0, p1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) p0[i] = __builtin_amdgcn_exp2f(sc[2 * kt][i]);
+        if (2 * kt + 1 <= LKB) {  // constant once the loop is unrolled
+#pragma unroll
+          for (int i = 0; i < 4; ++i) p1[i] = __builtin_amdgcn_exp2f(sc[2 * kt + 1][i]);
+        }
+        const half8_t pf = to_operand(p0, p1);
+        lacc = mfma16x16x32(ones, pf, lacc);
+#pragma unroll
+        for (int hb = 0; hb < HDB; ++hb) {
+          // V^T columns hold the keys of each 32-key step in the P operand's
+          // order (keys 32kt + 4g + i and 32kt + 16 + 4g + i at 32kt + 8g + i
+          // and + 4): one 16-byte read per fragment.
+          const half8_t vf = *reinterpret_cast<const half8_t*>(vt_lds + (vrow0 + 16 * hb + r16) * LD + 32 * kt + 8 * g);
+          o[hb] = mfma16x16x32(vf, pf, o[hb]);
+        }
+      }
+      if (exact || !__any(!(lacc[0] >= 1.0f && lacc[0] <= 0x1p20f))) break;
     }
     const float inv = MODE == 0 || lacc[0] > 0.f ? __builtin_amdgcn_rcpf(lacc[0]) : 0.f;
     if constexpr (HD >= 16) {

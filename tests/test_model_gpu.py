@@ -648,3 +648,46 @@ def test_fused_split_timeout_poisons_rows(pkg, cuda, geom, fault):
         with pytest.raises(RuntimeError, match="hand-off"):
             kernels.fused_forward_d128(xg, wpack, ppack, strict=True, **forced, **args)
         assert torch.equal(kernels.fused_forward_d128(xg, wpack, ppack, strict=True, **args), one)
+
+
+@pytest.mark.parametrize("geom", [(4, 128, 128, 4, 128, 2), (4, 128, 128, 16, 128, 2), (130, 128, 128, 4, 128, 1),
+                                  (3, 100, 128, 8, 128, 2)])
+@pytest.mark.parametrize("scores", ["overflow", "underflow"])
+def test_fused_stack_exact_softmax_fallback(pkg, cuda, geom, scores):
+    """The fused kernels exponentiate raw scores and fall back to the
+    max-subtracted softmax when a query's row sum leaves [1, 2^20].  Force
+    either exit from the host with q/k biases of +-3 over small q/k weights:
+    equal signs put every score far above zero (the FP16 probabilities
+    overflow), opposite signs far below (they underflow); the scores still
+    differ by the weights' small terms.  Split form (B <= 128) and
+    one-workgroup form (B = 130), head_dim 32, 8 and 16 (the last with a
+    padding mask), against the oracle and the per-op kernels; a fast path
+    taken wrongly would leave inf or NaN."""
+    config = pkg.TransformerConfig(*geom, True)
+    torch.manual_seed(1234)
+    baseline = BaselineTransformer(config).eval()
+    with torch.no_grad():
+        for layer in baseline.layers:
+            att = layer.attention
+            att.q_proj.weight.mul_(0.2)
+            att.k_proj.weight.mul_(0.2)
+            att.q_proj.bias.fill_(3.0 if scores == "overflow" else -3.0)
+            att.k_proj.bias.fill_(3.0)
+    optimized = pkg.UserOptimizedTransformer(config)
+    copy_model_weights(baseline, optimized)
+    optimized = optimized.to(cuda).eval()
+    b, s = geom[0], geom[1]
+    x = torch.randn(b, s, 128, generator=torch.Generator().manual_seed(91))
+    mask = _masks(b, s, 92)["mixed"] if geom[3] == 8 else None
+    xg = x.to(cuda)
+    mg = None if mask is None else mask.to(cuda)
+    assert optimized.execution_plan(b, s, padded=mask is not None).fused
+    with torch.inference_mode():
+        ref = baseline(x, mask)
+        fused = optimized(xg, mg).cpu()
+        optimized.enable_fused_stack(False)
+        per_op = optimized(xg, mg).cpu()
+        optimized.enable_fused_stack(True)
+    assert torch.isfinite(fused).all()
+    _check(ref, fused, f"fused {geom} {scores} scores")
+    torch.testing.assert_close(fused, per_op, atol=3e-3, rtol=1e-2)
