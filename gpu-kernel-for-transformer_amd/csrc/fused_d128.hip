@@ -509,12 +509,13 @@ __device__ __forceinline__ void attend16(const half_t* k_lds, const half_t* vt_l
     // out: softmax is invariant to that shift, and it is exact arithmetic as
     // long as the FP16 probabilities neither overflow nor all fall among
     // FP16's subnormals.  The row sum decides: an overflow makes it infinite,
-    // and a sum >= 1 puts the largest of at most 128 probabilities at >= 2^-7,
-    // so a subnormal one (< 2^-14, absolute error <= 2^-25) is off by at most
-    // 2^-18 of the largest, below FP16's own rounding.  Only when some query
-    // of the wave fails that test does the head run again in the textbook
-    // form, the row maximum subtracted first (and a query that sees no key
-    // at all, sum 0, gets its zero context there).
+    // and a sum >= 2^-4 puts the largest of at most 128 probabilities at
+    // >= 2^-11, so a subnormal one (< 2^-14, absolute error <= 2^-25) is off
+    // by at most 2^-14 of the largest, below FP16's own rounding of it
+    // (2^-11).  Only when some query of the wave fails that test does the
+    // head run again in the textbook form, the row maximum subtracted first
+    // (and a query that sees no key at all, sum 0, gets its zero context
+    // there).
     for (bool exact = false;; exact = true) {
       float4_t sc[LKB + 1];
 #pragma unroll
@@ -571,7 +572,7 @@ __device__ __forceinline__ void attend16(const half_t* k_lds, const half_t* vt_l
           o[hb] = mfma16x16x32(vf, pf, o[hb]);
         }
       }
-      if (exact || !__any(!(lacc[0] >= 1.0f && lacc[0] <= 0x1p20f))) break;
+      if (exact || !__any(!(lacc[0] >= 0x1p-4f && lacc[0] <= 0x1p20f))) break;
     }
     const float inv = MODE == 0 || lacc[0] > 0.f ? __builtin_amdgcn_rcpf(lacc[0]) : 0.f;
     if constexpr (HD >= 16) {

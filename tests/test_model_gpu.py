@@ -655,7 +655,7 @@ def test_fused_split_timeout_poisons_rows(pkg, cuda, geom, fault):
 @pytest.mark.parametrize("scores", ["overflow", "underflow"])
 def test_fused_stack_exact_softmax_fallback(pkg, cuda, geom, scores):
     """The fused kernels exponentiate raw scores and fall back to the
-    max-subtracted softmax when a query's row sum leaves [1, 2^20].  Force
+    max-subtracted softmax when a query's row sum leaves [2^-4, 2^20].  Force
     either exit from the host with q/k biases of +-3 over small q/k weights:
     equal signs put every score far above zero (the FP16 probabilities
     overflow), opposite signs far below (they underflow); the scores still
