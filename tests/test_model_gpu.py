@@ -691,3 +691,49 @@ def test_fused_stack_exact_softmax_fallback(pkg, cuda, geom, scores):
     assert torch.isfinite(fused).all()
     _check(ref, fused, f"fused {geom} {scores} scores")
     torch.testing.assert_close(fused, per_op, atol=3e-3, rtol=1e-2)
+
+
+def _random_geometries(count, seed):
+    """Seeded draws over the supported space: d_model 64-512, head_dim 8-256,
+    FFN width, layers, batch and ragged sequence lengths, causal or not,
+    padded or not; at most about 6k tokens so the CPU oracle stays quick."""
+    import random
+
+    rng = random.Random(seed)
+    out = []
+    while len(out) < count:
+        d = rng.choice([64, 128, 128, 256, 512])
+        hd = rng.choice([h for h in (8, 16, 32, 64, 128, 256) if h <= d])
+        f = rng.choice([d, 128, 2 * d]) if d != 128 else rng.choice([128, 128, 256])
+        s = rng.choice([1, 2, 17, 33, 64, 65, 96, 97, 100, 127, 128, 129, 160])
+        b = rng.choice([1, 2, 3, 5, 9, 16, 33, 64, 130])
+        if b * s > 6000:
+            continue
+        out.append((b, s, d, d // hd, f, rng.choice([1, 2, 3]), rng.random() < 0.75, rng.random() < 0.4))
+    return out
+
+
+@pytest.mark.parametrize("geom", _random_geometries(16, 2026))
+def test_random_geometries_against_oracle(pkg, cuda, geom):
+    """Seeded random geometries across the supported space (both the fused
+    d128 forms and the per-op kernels, every head width, ragged lengths,
+    causal or not, padded or not) against the oracle under the reference's
+    rule, with non-identity LayerNorm affine parameters."""
+    b, s, d, heads, f, layers, causal, padded = geom
+    if not causal and not padded:
+        padded = s > 1  # the non-causal forward is exercised with a mask too
+    config = pkg.TransformerConfig(b, s, d, heads, f, layers, causal)
+    baseline, optimized = _models(pkg, config, cuda)
+    with torch.no_grad():
+        g = torch.Generator().manual_seed(7)
+        for name, p in baseline.named_parameters():
+            if "norm" in name:
+                p.copy_(torch.randn(p.shape, generator=g) * 0.2 + (1.0 if name.endswith("weight") else 0.0))
+    copy_model_weights(baseline, optimized)
+    x, mask = generate_random_case(config, torch.device("cpu"), torch.float32, seed=31,
+                                   padding_ratio=0.4 if padded else 0.0)
+    with torch.inference_mode():
+        ref = baseline(x, mask)
+        out = optimized(x.to(cuda), mask.to(cuda)).cpu()
+    plan = optimized.execution_plan(b, s, padded=padded)
+    _check(ref, out, f"random geometry {geom} plan {plan.forward_strategy}")
