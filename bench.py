@@ -44,7 +44,8 @@ from the 16th on, so 5 warm-up steps alone leave the ramp inside the timed
 steps.  Then --warmup untimed steps and exactly --steps timed ones, with a
 device synchronisation on both sides.  The default of 100 timed steps (about
 0.19 s for cfg2) keeps one slow stretch of the clock from moving the
-headline: 20-step windows have read 1.855 and 1.915 ms on one box.
+headline: single 20-step windows of the same code read 1.855 and 1.915 ms
+in two runs.
 A config whose device-memory estimate exceeds --memory-fraction of the GPU is
 skipped before anything is allocated, and an out-of-memory error skips it
 (the reference's SAFE_SKIP / SAFE_ABORT, streamed_shape14.py:197-222); for the
