@@ -470,8 +470,9 @@ __device__ __forceinline__ void attend16(const half_t* k_lds, const half_t* vt_l
   // diagonal (key 4g + i after query r16), so the product leaves those
   // scores at -inf and no head masks them again.  Otherwise each head masks
   // its diagonal block after the product.  Both give the same values; the
-  // first is faster in the two-block (pair) form, the second in the split
-  // form.
+  // first is faster in the two-block (pair) form and in the one-block form
+  // at head_dim 16 and 8 (2 % per forward), the second in the one-block
+  // form at head_dim 64 (1 %).
   float4_t dstart = {0.f, 0.f, 0.f, 0.f};
   if constexpr (MODE != 2 && DSTART) {
 #pragma unroll
@@ -1021,15 +1022,16 @@ __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ 
         default: attend_pair<HD, HALF, 3, MASK>(L, qop, cop, g, r16); break;
       }
     } else {
+      constexpr bool SPLIT_DSTART = HD <= 16;
       switch (tb[0]) {
-        case 0: split::attend16<HD, HALF, 0, MASK>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16); break;
-        case 1: split::attend16<HD, HALF, 1, MASK>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16); break;
-        case 2: split::attend16<HD, HALF, 2, MASK>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16); break;
-        case 3: split::attend16<HD, HALF, 3, MASK>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16); break;
-        case 4: split::attend16<HD, HALF, 4, MASK>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16); break;
-        case 5: split::attend16<HD, HALF, 5, MASK>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16); break;
-        case 6: split::attend16<HD, HALF, 6, MASK>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16); break;
-        default: split::attend16<HD, HALF, 7, MASK>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16); break;
+        case 0: split::attend16<HD, HALF, 0, MASK, SPLIT_DSTART>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16); break;
+        case 1: split::attend16<HD, HALF, 1, MASK, SPLIT_DSTART>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16); break;
+        case 2: split::attend16<HD, HALF, 2, MASK, SPLIT_DSTART>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16); break;
+        case 3: split::attend16<HD, HALF, 3, MASK, SPLIT_DSTART>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16); break;
+        case 4: split::attend16<HD, HALF, 4, MASK, SPLIT_DSTART>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16); break;
+        case 5: split::attend16<HD, HALF, 5, MASK, SPLIT_DSTART>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16); break;
+        case 6: split::attend16<HD, HALF, 6, MASK, SPLIT_DSTART>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16); break;
+        default: split::attend16<HD, HALF, 7, MASK, SPLIT_DSTART>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16); break;
       }
     }
     lds_barrier();  // every wave is done with K and V^T: their areas take exchanges now
