@@ -452,32 +452,29 @@ struct Lds {
 // bytes kval (padding, and tokens past S).  MODE 2: no causal mask, key
 // validity only (every query block sees all eight key blocks).  In modes 1
 // and 2 a query may see no key at all: it then gets a zero context.
-template <int HD, int HALF, int QB, int MODE, bool DSTART = false>
-__device__ __forceinline__ void attend16(const half_t* k_lds, const half_t* vt_lds, const uint8_t* kval,
-                                         const half8_t (&qop)[OK], half8_t (&cop)[KS], int g_in, int r16_in) {
-  // Opaque copies: the lane-dependent head masks and addresses below are then
-  // rebuilt in each call instead of being hoisted out of the layer loop and
-  // spilled.
-  int g = g_in, r16 = r16_in;
-  asm volatile("" : "+v"(g), "+v"(r16));
+//
+// One pass over every head of the half.  EXACT false: the probabilities are
+// exp2 of the raw scores, with no row maximum taken out: softmax is
+// invariant to that shift, and it is exact arithmetic as long as the FP16
+// probabilities neither overflow nor all fall among FP16's subnormals.  The
+// row sum decides: an overflow makes it infinite, and a sum >= 2^-4 puts the
+// largest of at most 128 probabilities at >= 2^-11, so a subnormal one
+// (< 2^-14, absolute error <= 2^-25) is off by at most 2^-14 of the largest,
+// below FP16's own rounding of it (2^-11).  The pass returns whether any of
+// the lane's row sums (one per head) failed that test.  EXACT true: the
+// textbook form, the row maximum subtracted first (and a query that sees no
+// key at all, sum 0, gets its zero context).
+template <int HD, int HALF, int QB, int MODE, bool DSTART, bool EXACT>
+__device__ __forceinline__ bool attend16_pass(const half_t* k_lds, const half_t* vt_lds, const uint8_t* kval,
+                                              const half8_t (&qop)[OK], half8_t (&cop)[KS], int g, int r16,
+                                              float4_t dstart) {
   constexpr int H = D / HD;
   constexpr int HH = H / 2;
   constexpr int HDB = HD < 16 ? 1 : HD / 16;
   constexpr int KSH = HD >= 32 ? HD / 32 : 1;
   constexpr int LKB = MODE == 2 ? 7 : QB;  // last key block
   constexpr int NKT = LKB / 2 + 1;          // 32-key steps of the PV product
-  // DSTART: the diagonal block's score accumulators start at -inf above the
-  // diagonal (key 4g + i after query r16), so the product leaves those
-  // scores at -inf and no head masks them again.  Otherwise each head masks
-  // its diagonal block after the product.  Both give the same values; the
-  // first is faster in the two-block (pair) form and in the one-block form
-  // at head_dim 16 and 8 (2 % per forward), the second in the one-block
-  // form at head_dim 64 (1 %).
-  float4_t dstart = {0.f, 0.f, 0.f, 0.f};
-  if constexpr (MODE != 2 && DSTART) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) dstart[i] = 4 * g + i > r16 ? -INFINITY : 0.f;
-  }
+  bool bad = false;
 #pragma unroll
   for (int hh = 0; hh < HH; ++hh) {
     const int h = HH * HALF + hh;
@@ -505,76 +502,62 @@ __device__ __forceinline__ void attend16(const half_t* k_lds, const half_t* vt_l
     }
     const half8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
     const int vrow0 = HD < 16 ? 16 * (h / 2) : h * HD;
-    float4_t lacc, o[HDB];
-    // The probabilities are exp2 of the raw scores, with no row maximum taken
-    // out: softmax is invariant to that shift, and it is exact arithmetic as
-    // long as the FP16 probabilities neither overflow nor all fall among
-    // FP16's subnormals.  The row sum decides: an overflow makes it infinite,
-    // and a sum >= 2^-4 puts the largest of at most 128 probabilities at
-    // >= 2^-11, so a subnormal one (< 2^-14, absolute error <= 2^-25) is off
-    // by at most 2^-14 of the largest, below FP16's own rounding of it
-    // (2^-11).  Only when some query of the wave fails that test does the
-    // head run again in the textbook form, the row maximum subtracted first
-    // (and a query that sees no key at all, sum 0, gets its zero context
-    // there).
-    for (bool exact = false;; exact = true) {
-      float4_t sc[LKB + 1];
+    float4_t sc[LKB + 1];
 #pragma unroll
-      for (int kb = 0; kb <= LKB; ++kb) {
-        float4_t acc = MODE != 2 && DSTART && kb == QB ? dstart : float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int kb = 0; kb <= LKB; ++kb) {
+      float4_t acc = MODE != 2 && DSTART && kb == QB ? dstart : float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j < KSH; ++j) {
-          const half8_t kf = *reinterpret_cast<const half8_t*>(k_lds + (16 * kb + r16) * LD + 32 * (ks0 + j) + 8 * g);
-          acc = mfma16x16x32(kf, qh[j], acc);
-        }
-        if (MODE != 2 && !DSTART && kb == QB) {  // -inf above the diagonal: key 4g + i vs query r16
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (4 * g + i > r16) acc[i] = -INFINITY;
-        }
-        if constexpr (MODE != 0) {  // keys 16 kb + 4g .. +3: validity bytes
-          const uint32_t v4 = *reinterpret_cast<const uint32_t*>(kval + 16 * kb + 4 * g);
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (((v4 >> (8 * i)) & 0xffu) == 0u) acc[i] = -INFINITY;
-        }
-        sc[kb] = acc;
+      for (int j = 0; j < KSH; ++j) {
+        const half8_t kf = *reinterpret_cast<const half8_t*>(k_lds + (16 * kb + r16) * LD + 32 * (ks0 + j) + 8 * g);
+        acc = mfma16x16x32(kf, qh[j], acc);
       }
-      if (exact) {
-        float mx = -INFINITY;
+      if (MODE != 2 && !DSTART && kb == QB) {  // -inf above the diagonal: key 4g + i vs query r16
 #pragma unroll
-        for (int kb = 0; kb <= LKB; ++kb)
-          mx = fmaxf(mx, fmaxf(fmaxf(sc[kb][0], sc[kb][1]), fmaxf(sc[kb][2], sc[kb][3])));
-        mx = quad_group_max(mx);
-        if constexpr (MODE != 0) mx = mx == -INFINITY ? 0.f : mx;  // no visible key: every p is exp2(-inf) = 0
-#pragma unroll
-        for (int kb = 0; kb <= LKB; ++kb) sc[kb] -= mx;
+        for (int i = 0; i < 4; ++i)
+          if (4 * g + i > r16) acc[i] = -INFINITY;
       }
-      lacc = float4_t{0.f, 0.f, 0.f, 0.f};
+      if constexpr (MODE != 0) {  // keys 16 kb + 4g .. +3: validity bytes
+        const uint32_t v4 = *reinterpret_cast<const uint32_t*>(kval + 16 * kb + 4 * g);
 #pragma unroll
-      for (int hb = 0; hb < HDB; ++hb) o[hb] = float4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kt = 0; kt < NKT; ++kt) {
-        float4_t p0, p1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) p0[i] = __builtin_amdgcn_exp2f(sc[2 * kt][i]);
-        if (2 * kt + 1 <= LKB) {  // constant once the loop is unrolled
-#pragma unroll
-          for (int i = 0; i < 4; ++i) p1[i] = __builtin_amdgcn_exp2f(sc[2 * kt + 1][i]);
-        }
-        const half8_t pf = to_operand(p0, p1);
-        lacc = mfma16x16x32(ones, pf, lacc);
-#pragma unroll
-        for (int hb = 0; hb < HDB; ++hb) {
-          // V^T columns hold the keys of each 32-key step in the P operand's
-          // order (keys 32kt + 4g + i and 32kt + 16 + 4g + i at 32kt + 8g + i
-          // and + 4): one 16-byte read per fragment.
-          const half8_t vf = *reinterpret_cast<const half8_t*>(vt_lds + (vrow0 + 16 * hb + r16) * LD + 32 * kt + 8 * g);
-          o[hb] = mfma16x16x32(vf, pf, o[hb]);
-        }
+        for (int i = 0; i < 4; ++i)
+          if (((v4 >> (8 * i)) & 0xffu) == 0u) acc[i] = -INFINITY;
       }
-      if (exact || !__any(!(lacc[0] >= 0x1p-4f && lacc[0] <= 0x1p20f))) break;
+      sc[kb] = acc;
     }
+    if constexpr (EXACT) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb <= LKB; ++kb)
+        mx = fmaxf(mx, fmaxf(fmaxf(sc[kb][0], sc[kb][1]), fmaxf(sc[kb][2], sc[kb][3])));
+      mx = quad_group_max(mx);
+      if constexpr (MODE != 0) mx = mx == -INFINITY ? 0.f : mx;  // no visible key: every p is exp2(-inf) = 0
+#pragma unroll
+      for (int kb = 0; kb <= LKB; ++kb) sc[kb] -= mx;
+    }
+    float4_t lacc = {0.f, 0.f, 0.f, 0.f}, o[HDB];
+#pragma unroll
+    for (int hb = 0; hb < HDB; ++hb) o[hb] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kt = 0; kt < NKT; ++kt) {
+      float4_t p0, p1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p0[i] = __builtin_amdgcn_exp2f(sc[2 * kt][i]);
+      if (2 * kt + 1 <= LKB) {  // constant once the loop is unrolled
+#pragma unroll
+        for (int i = 0; i < 4; ++i) p1[i] = __builtin_amdgcn_exp2f(sc[2 * kt + 1][i]);
+      }
+      const half8_t pf = to_operand(p0, p1);
+      lacc = mfma16x16x32(ones, pf, lacc);
+#pragma unroll
+      for (int hb = 0; hb < HDB; ++hb) {
+        // V^T columns hold the keys of each 32-key step in the P operand's
+        // order (keys 32kt + 4g + i and 32kt + 16 + 4g + i at 32kt + 8g + i
+        // and + 4): one 16-byte read per fragment.
+        const half8_t vf = *reinterpret_cast<const half8_t*>(vt_lds + (vrow0 + 16 * hb + r16) * LD + 32 * kt + 8 * g);
+        o[hb] = mfma16x16x32(vf, pf, o[hb]);
+      }
+    }
+    if constexpr (!EXACT) bad |= !(lacc[0] >= 0x1p-4f && lacc[0] <= 0x1p20f);
     const float inv = MODE == 0 || lacc[0] > 0.f ? __builtin_amdgcn_rcpf(lacc[0]) : 0.f;
     if constexpr (HD >= 16) {
 #pragma unroll
@@ -594,11 +577,46 @@ __device__ __forceinline__ void attend16(const half_t* k_lds, const half_t* vt_l
       }
     }
     // Narrow heads: the scheduler may interleave two of them; four or eight
-    // measured no faster.
+    // measured no faster.  Wider heads run one at a time: with the textbook
+    // pass in the same function, two interleaved head_dim-32 heads need more
+    // than 256 VGPRs, and the spills cost more than the overlap gains.
     if constexpr (HD <= 16) {
       if (hh % 2 == 1) __builtin_amdgcn_sched_barrier(0);
+    } else {
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
+  return bad;
+}
+
+// Attention of query block QB for the heads of half HALF: the raw-exponent
+// pass over every head, then, only when a row sum of some head and query of
+// the wave failed its test (a wave vote, one per call), the textbook pass
+// over every head again, which overwrites the whole context.  One vote per
+// call rather than per head lets the heads' products and exponentials
+// interleave.
+// DSTART: the diagonal block's score accumulators start at -inf above the
+// diagonal (key 4g + i after query r16), so the product leaves those scores
+// at -inf and no head masks them again.  Otherwise each head masks its
+// diagonal block after the product.  Both give the same values; the first is
+// faster in the two-block (pair) form and in the one-block form at head_dim
+// 16 and 8 (2 % per forward), the second in the one-block form at head_dim
+// 64 (1 %).
+template <int HD, int HALF, int QB, int MODE, bool DSTART = false>
+__device__ __forceinline__ void attend16(const half_t* k_lds, const half_t* vt_lds, const uint8_t* kval,
+                                         const half8_t (&qop)[OK], half8_t (&cop)[KS], int g_in, int r16_in) {
+  // Opaque copies: the lane-dependent head masks and addresses are then
+  // rebuilt in each call instead of being hoisted out of the layer loop and
+  // spilled.
+  int g = g_in, r16 = r16_in;
+  asm volatile("" : "+v"(g), "+v"(r16));
+  float4_t dstart = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (MODE != 2 && DSTART) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dstart[i] = 4 * g + i > r16 ? -INFINITY : 0.f;
+  }
+  if (__any(attend16_pass<HD, HALF, QB, MODE, DSTART, false>(k_lds, vt_lds, kval, qop, cop, g, r16, dstart)))
+    attend16_pass<HD, HALF, QB, MODE, DSTART, true>(k_lds, vt_lds, kval, qop, cop, g, r16, dstart);
 }
 
 }  // namespace split

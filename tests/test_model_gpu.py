@@ -652,17 +652,19 @@ def test_fused_split_timeout_poisons_rows(pkg, cuda, geom, fault):
 
 @pytest.mark.parametrize("geom", [(4, 128, 128, 4, 128, 2), (4, 128, 128, 16, 128, 2), (130, 128, 128, 4, 128, 1),
                                   (3, 100, 128, 8, 128, 2)])
-@pytest.mark.parametrize("scores", ["overflow", "underflow"])
+@pytest.mark.parametrize("scores", ["overflow", "underflow", "one_head"])
 def test_fused_stack_exact_softmax_fallback(pkg, cuda, geom, scores):
     """The fused kernels exponentiate raw scores and fall back to the
     max-subtracted softmax when a query's row sum leaves [2^-4, 2^20].  Force
     either exit from the host with q/k biases of +-3 over small q/k weights:
     equal signs put every score far above zero (the FP16 probabilities
     overflow), opposite signs far below (they underflow); the scores still
-    differ by the weights' small terms.  Split form (B <= 128) and
-    one-workgroup form (B = 130), head_dim 32, 8 and 16 (the last with a
-    padding mask), against the oracle and the per-op kernels; a fast path
-    taken wrongly would leave inf or NaN."""
+    differ by the weights' small terms.  "one_head" raises only head 0's
+    scores, so that head's failure sends every head of its half, block by
+    block, through the textbook pass while the other half stays on the fast
+    one.  Split form (B <= 128) and one-workgroup form (B = 130), head_dim
+    32, 8 and 16 (the last with a padding mask), against the oracle and the
+    per-op kernels; a fast path taken wrongly would leave inf or NaN."""
     config = pkg.TransformerConfig(*geom, True)
     torch.manual_seed(1234)
     baseline = BaselineTransformer(config).eval()
@@ -671,8 +673,13 @@ def test_fused_stack_exact_softmax_fallback(pkg, cuda, geom, scores):
             att = layer.attention
             att.q_proj.weight.mul_(0.2)
             att.k_proj.weight.mul_(0.2)
-            att.q_proj.bias.fill_(3.0 if scores == "overflow" else -3.0)
-            att.k_proj.bias.fill_(3.0)
+            if scores == "one_head":
+                hd = geom[2] // geom[3]
+                att.q_proj.bias[:hd] = 3.0
+                att.k_proj.bias[:hd] = 3.0
+            else:
+                att.q_proj.bias.fill_(3.0 if scores == "overflow" else -3.0)
+                att.k_proj.bias.fill_(3.0)
     optimized = pkg.UserOptimizedTransformer(config)
     copy_model_weights(baseline, optimized)
     optimized = optimized.to(cuda).eval()
