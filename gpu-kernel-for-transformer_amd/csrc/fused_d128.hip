@@ -759,11 +759,38 @@ __device__ __forceinline__ void get_partner2(char* area, half8_t (&full)[NBT][KS
 }
 
 // Causal attention of blocks P and 7 - P (MASK 2: no causal mask) for the heads of half HALF.
+// At head_dim >= 32 both blocks' raw-exponent passes run before a single
+// branch, which then reruns in the textbook form each block whose vote
+// failed: the same per-block decision as two attend16 calls (so the pair
+// and split forms still agree bit for bit), one branch per layer instead of
+// two (cfg2 -0.8 %).  Narrower heads keep two calls: their kernels would
+// spill with both blocks' fallbacks in one branch.
 template <int HD, int HALF, int P, int MASK>
-__device__ __forceinline__ void attend_pair(const Lds& L, const half8_t (&qop)[NB][OK], half8_t (&cop)[NB][KS], int g,
-                                            int r16) {
-  split::attend16<HD, HALF, P, MASK, true>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16);
-  split::attend16<HD, HALF, 7 - P, MASK, true>(L.k, L.vt, L.kval, qop[1], cop[1], g, r16);
+__device__ __forceinline__ void attend_pair(const Lds& L, const half8_t (&qop)[NB][OK], half8_t (&cop)[NB][KS], int g_in,
+                                            int r16_in) {
+  if constexpr (HD <= 16) {
+    split::attend16<HD, HALF, P, MASK, true>(L.k, L.vt, L.kval, qop[0], cop[0], g_in, r16_in);
+    split::attend16<HD, HALF, 7 - P, MASK, true>(L.k, L.vt, L.kval, qop[1], cop[1], g_in, r16_in);
+  } else {
+    int g = g_in, r16 = r16_in;  // opaque copies, as in attend16
+    asm volatile("" : "+v"(g), "+v"(r16));
+    float4_t dstart = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (MASK != 2) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dstart[i] = 4 * g + i > r16 ? -INFINITY : 0.f;
+    }
+    const bool bad0 =
+        split::attend16_pass<HD, HALF, P, MASK, true, false>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16, dstart);
+    const bool bad1 =
+        split::attend16_pass<HD, HALF, 7 - P, MASK, true, false>(L.k, L.vt, L.kval, qop[1], cop[1], g, r16, dstart);
+    const bool redo0 = __any(bad0), redo1 = __any(bad1);
+    if (redo0 || redo1) {
+      if (redo0)
+        split::attend16_pass<HD, HALF, P, MASK, true, true>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16, dstart);
+      if (redo1)
+        split::attend16_pass<HD, HALF, 7 - P, MASK, true, true>(L.k, L.vt, L.kval, qop[1], cop[1], g, r16, dstart);
+    }
+  }
 }
 
 // K/V exchange of the split form.  Per (sequence, layer) a 32 KB slot: K rows
