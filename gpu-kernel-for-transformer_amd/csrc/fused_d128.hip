@@ -464,6 +464,118 @@ struct Lds {
 // the lane's row sums (one per head) failed that test.  EXACT true: the
 // textbook form, the row maximum subtracted first (and a query that sees no
 // key at all, sum 0, gets its zero context).
+// One head: scores of query block QB against key blocks 0..LKB (the
+// head's Q k-steps qh, masked to the head for head_dim < 32, against K
+// columns from k-step ks0), exponentials, row sums and the PV product into
+// o (V^T rows from vrow0).
+template <int HD, int QB, int MODE, bool DSTART, bool EXACT>
+__device__ __forceinline__ void attend_head(const half_t* k_lds, const half_t* vt_lds, const uint8_t* kval,
+                                            const half8_t (&qh)[HD >= 32 ? HD / 32 : 1], int ks0, int vrow0, int g,
+                                            int r16, float4_t dstart, float4_t& lacc,
+                                            float4_t (&o)[HD < 16 ? 1 : HD / 16]) {
+  constexpr int HDB = HD < 16 ? 1 : HD / 16;
+  constexpr int KSH = HD >= 32 ? HD / 32 : 1;
+  constexpr int LKB = MODE == 2 ? 7 : QB;  // last key block
+  constexpr int NKT = LKB / 2 + 1;          // 32-key steps of the PV product
+  const half8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
+  float4_t sc[LKB + 1];
+#pragma unroll
+  for (int kb = 0; kb <= LKB; ++kb) {
+    float4_t acc = MODE != 2 && DSTART && kb == QB ? dstart : float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < KSH; ++j) {
+      const half8_t kf = *reinterpret_cast<const half8_t*>(k_lds + (16 * kb + r16) * LD + 32 * (ks0 + j) + 8 * g);
+      acc = mfma16x16x32(kf, qh[j], acc);
+    }
+    if (MODE != 2 && !DSTART && kb == QB) {  // -inf above the diagonal: key 4g + i vs query r16
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (4 * g + i > r16) acc[i] = -INFINITY;
+    }
+    if constexpr (MODE != 0) {  // keys 16 kb + 4g .. +3: validity bytes
+      const uint32_t v4 = *reinterpret_cast<const uint32_t*>(kval + 16 * kb + 4 * g);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (((v4 >> (8 * i)) & 0xffu) == 0u) acc[i] = -INFINITY;
+    }
+    sc[kb] = acc;
+  }
+  if constexpr (EXACT) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb <= LKB; ++kb)
+      mx = fmaxf(mx, fmaxf(fmaxf(sc[kb][0], sc[kb][1]), fmaxf(sc[kb][2], sc[kb][3])));
+    mx = quad_group_max(mx);
+    if constexpr (MODE != 0) mx = mx == -INFINITY ? 0.f : mx;  // no visible key: every p is exp2(-inf) = 0
+#pragma unroll
+    for (int kb = 0; kb <= LKB; ++kb) sc[kb] -= mx;
+  }
+  lacc = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int hb = 0; hb < HDB; ++hb) o[hb] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int kt = 0; kt < NKT; ++kt) {
+    float4_t p0, p1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p0[i] = __builtin_amdgcn_exp2f(sc[2 * kt][i]);
+    if (2 * kt + 1 <= LKB) {  // constant once the loop is unrolled
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p1[i] = __builtin_amdgcn_exp2f(sc[2 * kt + 1][i]);
+    }
+    const half8_t pf = to_operand(p0, p1);
+    lacc = mfma16x16x32(ones, pf, lacc);
+#pragma unroll
+    for (int hb = 0; hb < HDB; ++hb) {
+      // V^T columns hold the keys of each 32-key step in the P operand's
+      // order (keys 32kt + 4g + i and 32kt + 16 + 4g + i at 32kt + 8g + i
+      // and + 4): one 16-byte read per fragment.
+      const half8_t vf = *reinterpret_cast<const half8_t*>(vt_lds + (vrow0 + 16 * hb + r16) * LD + 32 * kt + 8 * g);
+      o[hb] = mfma16x16x32(vf, pf, o[hb]);
+    }
+  }
+}
+
+// Keep only the features of head hrel (within its 32-feature k-step) of a Q
+// k-step.  The lane's low four halves are features 4g..4g+3 of the k-step,
+// its high four 16+4g..16+4g+3, so each group lies in one head: zero a whole
+// 32-bit word pair instead of selecting half by half.
+template <int HD>
+__device__ __forceinline__ half8_t head_mask(half8_t q, int hrel, int g) {
+  typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+  const bool keep_lo = HD == 16 ? hrel == 0 : (g >> 1) == hrel;
+  const bool keep_hi = HD == 16 ? hrel == 1 : (g >> 1) + 2 == hrel;
+  u32x4_t w = __builtin_bit_cast(u32x4_t, q);
+  w[0] = keep_lo ? w[0] : 0u;
+  w[1] = keep_lo ? w[1] : 0u;
+  w[2] = keep_hi ? w[2] : 0u;
+  w[3] = keep_hi ? w[3] : 0u;
+  return __builtin_bit_cast(half8_t, w);
+}
+
+// Each row sum is tested as described below; true when the lane's failed.
+__device__ __forceinline__ bool row_sum_fails(const float4_t& lacc) {
+  return !(lacc[0] >= 0x1p-4f && lacc[0] <= 0x1p20f);
+}
+
+// One pass over every head of the half.  EXACT false: the probabilities are
+// exp2 of the raw scores, with no row maximum taken out: softmax is
+// invariant to that shift, and it is exact arithmetic as long as the FP16
+// probabilities neither overflow nor all fall among FP16's subnormals.  The
+// row sum decides: an overflow makes it infinite, and a sum >= 2^-4 puts the
+// largest of at most 128 probabilities at >= 2^-11, so a subnormal one
+// (< 2^-14, absolute error <= 2^-25) is off by at most 2^-14 of the largest,
+// below FP16's own rounding of it (2^-11).  The pass returns whether any of
+// the lane's row sums (one per head) failed that test.  EXACT true: the
+// textbook form, the row maximum subtracted first (and a query that sees no
+// key at all, sum 0, gets its zero context).
+//
+// head_dim <= 16: a loop (not unrolled) over the half's two own k-steps,
+// each holding 32 / HD heads, unrolled.  That halves the attention code of
+// these kernels (the sixteen-head split kernel was 140 KB, and each launch
+// of its 128 workgroups fetches its code into the instruction caches anew),
+// and the head within its k-step stays a constant, so the head masks and
+// the context positions do too; only the k-step's Q operand and context
+// slot are picked at run time (a wave-uniform select).
 template <int HD, int HALF, int QB, int MODE, bool DSTART, bool EXACT>
 __device__ __forceinline__ bool attend16_pass(const half_t* k_lds, const half_t* vt_lds, const uint8_t* kval,
                                               const half8_t (&qop)[OK], half8_t (&cop)[KS], int g, int r16,
@@ -472,94 +584,56 @@ __device__ __forceinline__ bool attend16_pass(const half_t* k_lds, const half_t*
   constexpr int HH = H / 2;
   constexpr int HDB = HD < 16 ? 1 : HD / 16;
   constexpr int KSH = HD >= 32 ? HD / 32 : 1;
-  constexpr int LKB = MODE == 2 ? 7 : QB;  // last key block
-  constexpr int NKT = LKB / 2 + 1;          // 32-key steps of the PV product
   bool bad = false;
+  if constexpr (HD <= 16) {
+    static_assert(OK == 2, "two own k-steps per half");
+    constexpr int HPK = 32 / HD;  // heads per k-step
+#pragma unroll 1
+    for (int kk = 0; kk < OK; ++kk) {
+      const half8_t qk = kk == 0 ? qop[0] : qop[1];
+      const int ks0 = OK * HALF + kk;
+      half8_t ck = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-  for (int hh = 0; hh < HH; ++hh) {
-    const int h = HH * HALF + hh;
-    const int ks0 = (h * HD) / 32;
-    half8_t qh[KSH];
+      for (int hk = 0; hk < HPK; ++hk) {
+        const half8_t qh[1] = {head_mask<HD>(qk, hk, g)};
+        const int h = HPK * ks0 + hk;
+        const int vrow0 = HD < 16 ? 16 * (h / 2) : h * HD;
+        float4_t lacc, o[HDB];
+        attend_head<HD, QB, MODE, DSTART, EXACT>(k_lds, vt_lds, kval, qh, ks0, vrow0, g, r16, dstart, lacc, o);
+        if constexpr (!EXACT) bad |= row_sum_fails(lacc);
+        const float inv = MODE == 0 || lacc[0] > 0.f ? __builtin_amdgcn_rcpf(lacc[0]) : 0.f;
+        if constexpr (HD == 16) {
+          // Head hk fills V^T row block h: the k-step's low (hk even) or high four halves.
+          const half4_t v = to_half4(o[0] * inv);
 #pragma unroll
-    for (int j = 0; j < KSH; ++j) {
-      qh[j] = qop[ks0 + j - OK * HALF];
-      if constexpr (HD < 32) {
-        // Keep only this head's features of the shared k-step.  The lane's
-        // low four halves are features 4g..4g+3 of the k-step, its high four
-        // 16+4g..16+4g+3, so each group lies in one head: zero a whole
-        // 32-bit word pair instead of selecting half by half.
-        typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-        const int hrel = h % (32 / HD);  // head within the k-step
-        const bool keep_lo = HD == 16 ? hrel == 0 : (g >> 1) == hrel;
-        const bool keep_hi = HD == 16 ? hrel == 1 : (g >> 1) + 2 == hrel;
-        u32x4_t w = __builtin_bit_cast(u32x4_t, qh[j]);
-        w[0] = keep_lo ? w[0] : 0u;
-        w[1] = keep_lo ? w[1] : 0u;
-        w[2] = keep_hi ? w[2] : 0u;
-        w[3] = keep_hi ? w[3] : 0u;
-        qh[j] = __builtin_bit_cast(half8_t, w);
+          for (int i = 0; i < 4; ++i) ck[4 * (hk & 1) + i] = v[i];
+        } else {
+          // Two 8-wide heads share one 16-row block (hk / 2): rows 0-7 (g < 2) are the even head's.
+          if ((g / 2) == (hk & 1)) {
+            const half4_t v = to_half4(o[0] * inv);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) ck[4 * ((hk / 2) & 1) + i] = v[i];
+          }
+        }
+        // The scheduler may interleave two heads; four or eight measured no faster.
+        if (hk % 2 == 1) __builtin_amdgcn_sched_barrier(0);
       }
+      cop[OK * HALF] = kk == 0 ? ck : cop[OK * HALF];
+      cop[OK * HALF + 1] = kk == 1 ? ck : cop[OK * HALF + 1];
     }
-    const half8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
-    const int vrow0 = HD < 16 ? 16 * (h / 2) : h * HD;
-    float4_t sc[LKB + 1];
+  } else {
 #pragma unroll
-    for (int kb = 0; kb <= LKB; ++kb) {
-      float4_t acc = MODE != 2 && DSTART && kb == QB ? dstart : float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int hh = 0; hh < HH; ++hh) {
+      const int h = HH * HALF + hh;
+      const int ks0 = (h * HD) / 32;
+      half8_t qh[KSH];
 #pragma unroll
-      for (int j = 0; j < KSH; ++j) {
-        const half8_t kf = *reinterpret_cast<const half8_t*>(k_lds + (16 * kb + r16) * LD + 32 * (ks0 + j) + 8 * g);
-        acc = mfma16x16x32(kf, qh[j], acc);
-      }
-      if (MODE != 2 && !DSTART && kb == QB) {  // -inf above the diagonal: key 4g + i vs query r16
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (4 * g + i > r16) acc[i] = -INFINITY;
-      }
-      if constexpr (MODE != 0) {  // keys 16 kb + 4g .. +3: validity bytes
-        const uint32_t v4 = *reinterpret_cast<const uint32_t*>(kval + 16 * kb + 4 * g);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (((v4 >> (8 * i)) & 0xffu) == 0u) acc[i] = -INFINITY;
-      }
-      sc[kb] = acc;
-    }
-    if constexpr (EXACT) {
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kb = 0; kb <= LKB; ++kb)
-        mx = fmaxf(mx, fmaxf(fmaxf(sc[kb][0], sc[kb][1]), fmaxf(sc[kb][2], sc[kb][3])));
-      mx = quad_group_max(mx);
-      if constexpr (MODE != 0) mx = mx == -INFINITY ? 0.f : mx;  // no visible key: every p is exp2(-inf) = 0
-#pragma unroll
-      for (int kb = 0; kb <= LKB; ++kb) sc[kb] -= mx;
-    }
-    float4_t lacc = {0.f, 0.f, 0.f, 0.f}, o[HDB];
-#pragma unroll
-    for (int hb = 0; hb < HDB; ++hb) o[hb] = float4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kt = 0; kt < NKT; ++kt) {
-      float4_t p0, p1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) p0[i] = __builtin_amdgcn_exp2f(sc[2 * kt][i]);
-      if (2 * kt + 1 <= LKB) {  // constant once the loop is unrolled
-#pragma unroll
-        for (int i = 0; i < 4; ++i) p1[i] = __builtin_amdgcn_exp2f(sc[2 * kt + 1][i]);
-      }
-      const half8_t pf = to_operand(p0, p1);
-      lacc = mfma16x16x32(ones, pf, lacc);
-#pragma unroll
-      for (int hb = 0; hb < HDB; ++hb) {
-        // V^T columns hold the keys of each 32-key step in the P operand's
-        // order (keys 32kt + 4g + i and 32kt + 16 + 4g + i at 32kt + 8g + i
-        // and + 4): one 16-byte read per fragment.
-        const half8_t vf = *reinterpret_cast<const half8_t*>(vt_lds + (vrow0 + 16 * hb + r16) * LD + 32 * kt + 8 * g);
-        o[hb] = mfma16x16x32(vf, pf, o[hb]);
-      }
-    }
-    if constexpr (!EXACT) bad |= !(lacc[0] >= 0x1p-4f && lacc[0] <= 0x1p20f);
-    const float inv = MODE == 0 || lacc[0] > 0.f ? __builtin_amdgcn_rcpf(lacc[0]) : 0.f;
-    if constexpr (HD >= 16) {
+      for (int j = 0; j < KSH; ++j) qh[j] = qop[ks0 + j - OK * HALF];
+      const int vrow0 = h * HD;
+      float4_t lacc, o[HDB];
+      attend_head<HD, QB, MODE, DSTART, EXACT>(k_lds, vt_lds, kval, qh, ks0, vrow0, g, r16, dstart, lacc, o);
+      if constexpr (!EXACT) bad |= row_sum_fails(lacc);
+      const float inv = MODE == 0 || lacc[0] > 0.f ? __builtin_amdgcn_rcpf(lacc[0]) : 0.f;
 #pragma unroll
       for (int hb = 0; hb < HDB; ++hb) {
         const int c = (vrow0 + 16 * hb) / 16;
@@ -567,22 +641,9 @@ __device__ __forceinline__ bool attend16_pass(const half_t* k_lds, const half_t*
 #pragma unroll
         for (int i = 0; i < 4; ++i) cop[c / 2][4 * (c & 1) + i] = v[i];
       }
-    } else {
-      // Two 8-wide heads share one 16-row block: rows 0-7 (g < 2) are the even head's.
-      const int c = vrow0 / 16;
-      if ((g / 2) == (h & 1)) {
-        const half4_t v = to_half4(o[0] * inv);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) cop[c / 2][4 * (c & 1) + i] = v[i];
-      }
-    }
-    // Narrow heads: the scheduler may interleave two of them; four or eight
-    // measured no faster.  Wider heads run one at a time: with the textbook
-    // pass in the same function, two interleaved head_dim-32 heads need more
-    // than 256 VGPRs, and the spills cost more than the overlap gains.
-    if constexpr (HD <= 16) {
-      if (hh % 2 == 1) __builtin_amdgcn_sched_barrier(0);
-    } else {
+      // Heads run one at a time: with the textbook pass in the same function,
+      // two interleaved head_dim-32 heads need more than 256 VGPRs, and the
+      // spills cost more than the overlap gains.
       __builtin_amdgcn_sched_barrier(0);
     }
   }
