@@ -441,33 +441,20 @@ struct Lds {
   int poison;                                          // split form: a K/V hand-off of this block timed out
 };
 
-// Causal attention of query block QB (keys 0 .. 16 QB + 15) for the heads of
-// half HALF.  S^T = K . Q^T (M = keys, N = queries): lane holds keys
-// 16kb + 4g + i of query r16, which with the key order 32kt + 4g + (m&3) +
-// 16(m>>2) is the B operand of O^T = V^T . P^T directly.  All scores of a
-// query fit in registers, so the softmax needs no running rescale; row sums
-// come from an all-ones A operand.  The context leaves as MFMA operands in
-// the permuted k order (cop, own k-steps only).
+// Causal attention of query block QB (keys 0 .. 16 QB + 15), one head:
+// scores against key blocks 0..LKB (the head's Q k-steps qh, masked to the
+// head for head_dim < 32, against K columns from k-step ks0), exponentials,
+// row sums and the PV product into o (V^T rows from vrow0).
+// S^T = K . Q^T (M = keys, N = queries): lane holds keys 16kb + 4g + i of
+// query r16, which with the key order 32kt + 4g + (m&3) + 16(m>>2) is the B
+// operand of O^T = V^T . P^T directly.  All scores of a query fit in
+// registers, so the softmax needs no running rescale; row sums come from an
+// all-ones A operand.
 // MODE 0: causal, every key valid.  MODE 1: causal plus the key validity
 // bytes kval (padding, and tokens past S).  MODE 2: no causal mask, key
 // validity only (every query block sees all eight key blocks).  In modes 1
 // and 2 a query may see no key at all: it then gets a zero context.
-//
-// One pass over every head of the half.  EXACT false: the probabilities are
-// exp2 of the raw scores, with no row maximum taken out: softmax is
-// invariant to that shift, and it is exact arithmetic as long as the FP16
-// probabilities neither overflow nor all fall among FP16's subnormals.  The
-// row sum decides: an overflow makes it infinite, and a sum >= 2^-4 puts the
-// largest of at most 128 probabilities at >= 2^-11, so a subnormal one
-// (< 2^-14, absolute error <= 2^-25) is off by at most 2^-14 of the largest,
-// below FP16's own rounding of it (2^-11).  The pass returns whether any of
-// the lane's row sums (one per head) failed that test.  EXACT true: the
-// textbook form, the row maximum subtracted first (and a query that sees no
-// key at all, sum 0, gets its zero context).
-// One head: scores of query block QB against key blocks 0..LKB (the
-// head's Q k-steps qh, masked to the head for head_dim < 32, against K
-// columns from k-step ks0), exponentials, row sums and the PV product into
-// o (V^T rows from vrow0).
+// EXACT: subtract the row maximum before exp2 (attend16_pass says when).
 template <int HD, int QB, int MODE, bool DSTART, bool EXACT>
 __device__ __forceinline__ void attend_head(const half_t* k_lds, const half_t* vt_lds, const uint8_t* kval,
                                             const half8_t (&qh)[HD >= 32 ? HD / 32 : 1], int ks0, int vrow0, int g,
@@ -557,7 +544,9 @@ __device__ __forceinline__ bool row_sum_fails(const float4_t& lacc) {
   return !(lacc[0] >= 0x1p-4f && lacc[0] <= 0x1p20f);
 }
 
-// One pass over every head of the half.  EXACT false: the probabilities are
+// One pass over every head of half HALF for query block QB; the context
+// leaves as MFMA operands in the permuted k order (cop, own k-steps only).
+// EXACT false: the probabilities are
 // exp2 of the raw scores, with no row maximum taken out: softmax is
 // invariant to that shift, and it is exact arithmetic as long as the FP16
 // probabilities neither overflow nor all fall among FP16's subnormals.  The
