@@ -437,6 +437,7 @@ struct Lds {
   __attribute__((aligned(1024))) char wst[2][MAT_BYTES];  // weight matrix stages
   float prm[2][P_LAYER];                               // per-layer vectors, by layer parity
   float2 xstat[2][XSTAT];                              // LayerNorm partial statistics (LN1 / LN2)
+  __attribute__((aligned(16))) half_t ones[128];       // head_dim 8: FP16 ones, the PV product's row-sum rows
   uint8_t kval[SMAX];                                  // MASKED: token t may be attended to / is output
   int poison;                                          // split form: a K/V hand-off of this block timed out
 };
@@ -457,9 +458,9 @@ struct Lds {
 // EXACT: subtract the row maximum before exp2 (attend16_pass says when).
 template <int HD, int QB, int MODE, bool DSTART, bool EXACT>
 __device__ __forceinline__ void attend_head(const half_t* k_lds, const half_t* vt_lds, const uint8_t* kval,
-                                            const half8_t (&qh)[HD >= 32 ? HD / 32 : 1], int ks0, int vrow0, int g,
-                                            int r16, float4_t dstart, float4_t& lacc,
-                                            float4_t (&o)[HD < 16 ? 1 : HD / 16]) {
+                                            const half_t* ones_lds, const half8_t (&qh)[HD >= 32 ? HD / 32 : 1],
+                                            int ks0, int vrow0, int hpar, int g, int r16, float4_t dstart,
+                                            float4_t& lacc, float4_t (&o)[HD < 16 ? 1 : HD / 16]) {
   constexpr int HDB = HD < 16 ? 1 : HD / 16;
   constexpr int KSH = HD >= 32 ? HD / 32 : 1;
   constexpr int LKB = MODE == 2 ? 7 : QB;  // last key block
@@ -500,6 +501,12 @@ __device__ __forceinline__ void attend_head(const half_t* k_lds, const half_t* v
   lacc = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int hb = 0; hb < HDB; ++hb) o[hb] = float4_t{0.f, 0.f, 0.f, 0.f};
+  // head_dim 8: the 16 V^T rows of the head's block are two heads' features,
+  // and the product's rows of the other head would be discarded.  Those A
+  // rows (lanes r16 / 8 != the head's parity) read FP16 ones instead, so the
+  // same product leaves the row sums there: the separate all-ones product
+  // goes away, with the same products summed in the same order.
+  const half_t* vrow = HD == 8 && (r16 >> 3) != hpar ? ones_lds : vt_lds + (vrow0 + r16) * LD + 8 * g;
 #pragma unroll
   for (int kt = 0; kt < NKT; ++kt) {
     float4_t p0, p1 = {0.f, 0.f, 0.f, 0.f};
@@ -510,15 +517,25 @@ __device__ __forceinline__ void attend_head(const half_t* k_lds, const half_t* v
       for (int i = 0; i < 4; ++i) p1[i] = __builtin_amdgcn_exp2f(sc[2 * kt + 1][i]);
     }
     const half8_t pf = to_operand(p0, p1);
-    lacc = mfma16x16x32(ones, pf, lacc);
+    if constexpr (HD != 8) lacc = mfma16x16x32(ones, pf, lacc);
 #pragma unroll
     for (int hb = 0; hb < HDB; ++hb) {
       // V^T columns hold the keys of each 32-key step in the P operand's
       // order (keys 32kt + 4g + i and 32kt + 16 + 4g + i at 32kt + 8g + i
       // and + 4): one 16-byte read per fragment.
-      const half8_t vf = *reinterpret_cast<const half8_t*>(vt_lds + (vrow0 + 16 * hb + r16) * LD + 32 * kt + 8 * g);
+      const half8_t vf = *reinterpret_cast<const half8_t*>(vrow + 16 * hb * LD + 32 * kt);
       o[hb] = mfma16x16x32(vf, pf, o[hb]);
     }
+  }
+  if constexpr (HD == 8) {
+    // Lane (g, r16) holds rows 4g..4g+3 of query r16: the head's features for
+    // g / 2 == its parity, the row sum otherwise.  Lane l ^ 32 is (g ^ 2, r16):
+    // the swap's first result holds lane l's value for l < 32 and lane
+    // l - 32's above, its second lane l + 32's below and lane l's above, so
+    // an even head's sum is the second for every lane and an odd head's the first.
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(o[0][0]), __float_as_uint(o[0][0]), false, false);
+    const float sum = __uint_as_float(hpar ? r[0] : r[1]);
+    lacc = float4_t{sum, sum, sum, sum};
   }
 }
 
@@ -567,8 +584,8 @@ __device__ __forceinline__ bool row_sum_fails(const float4_t& lacc) {
 // slot are picked at run time (a wave-uniform select).
 template <int HD, int HALF, int QB, int MODE, bool DSTART, bool EXACT>
 __device__ __forceinline__ bool attend16_pass(const half_t* k_lds, const half_t* vt_lds, const uint8_t* kval,
-                                              const half8_t (&qop)[OK], half8_t (&cop)[KS], int g, int r16,
-                                              float4_t dstart) {
+                                              const half_t* ones_lds, const half8_t (&qop)[OK], half8_t (&cop)[KS],
+                                              int g, int r16, float4_t dstart) {
   constexpr int H = D / HD;
   constexpr int HH = H / 2;
   constexpr int HDB = HD < 16 ? 1 : HD / 16;
@@ -588,7 +605,8 @@ __device__ __forceinline__ bool attend16_pass(const half_t* k_lds, const half_t*
         const int h = HPK * ks0 + hk;
         const int vrow0 = HD < 16 ? 16 * (h / 2) : h * HD;
         float4_t lacc, o[HDB];
-        attend_head<HD, QB, MODE, DSTART, EXACT>(k_lds, vt_lds, kval, qh, ks0, vrow0, g, r16, dstart, lacc, o);
+        attend_head<HD, QB, MODE, DSTART, EXACT>(k_lds, vt_lds, kval, ones_lds, qh, ks0, vrow0, hk & 1, g, r16,
+                                                 dstart, lacc, o);
         if constexpr (!EXACT) bad |= row_sum_fails(lacc);
         const float inv = MODE == 0 || lacc[0] > 0.f ? __builtin_amdgcn_rcpf(lacc[0]) : 0.f;
         if constexpr (HD == 16) {
@@ -620,7 +638,8 @@ __device__ __forceinline__ bool attend16_pass(const half_t* k_lds, const half_t*
       for (int j = 0; j < KSH; ++j) qh[j] = qop[ks0 + j - OK * HALF];
       const int vrow0 = h * HD;
       float4_t lacc, o[HDB];
-      attend_head<HD, QB, MODE, DSTART, EXACT>(k_lds, vt_lds, kval, qh, ks0, vrow0, g, r16, dstart, lacc, o);
+      attend_head<HD, QB, MODE, DSTART, EXACT>(k_lds, vt_lds, kval, ones_lds, qh, ks0, vrow0, h & 1, g, r16, dstart,
+                                               lacc, o);
       if constexpr (!EXACT) bad |= row_sum_fails(lacc);
       const float inv = MODE == 0 || lacc[0] > 0.f ? __builtin_amdgcn_rcpf(lacc[0]) : 0.f;
 #pragma unroll
@@ -654,7 +673,8 @@ __device__ __forceinline__ bool attend16_pass(const half_t* k_lds, const half_t*
 // 64 (1 %).
 template <int HD, int HALF, int QB, int MODE, bool DSTART = false>
 __device__ __forceinline__ void attend16(const half_t* k_lds, const half_t* vt_lds, const uint8_t* kval,
-                                         const half8_t (&qop)[OK], half8_t (&cop)[KS], int g_in, int r16_in) {
+                                         const half_t* ones_lds, const half8_t (&qop)[OK], half8_t (&cop)[KS],
+                                         int g_in, int r16_in) {
   // Opaque copies: the lane-dependent head masks and addresses are then
   // rebuilt in each call instead of being hoisted out of the layer loop and
   // spilled.
@@ -668,8 +688,10 @@ __device__ __forceinline__ void attend16(const half_t* k_lds, const half_t* vt_l
   // Marked unlikely, so that the textbook pass is laid out away from the hot
   // code (fewer instruction-cache lines in the loop; 0.3-1.1 % per forward).
   if (__builtin_expect(
-          __any(attend16_pass<HD, HALF, QB, MODE, DSTART, false>(k_lds, vt_lds, kval, qop, cop, g, r16, dstart)), 0))
-    attend16_pass<HD, HALF, QB, MODE, DSTART, true>(k_lds, vt_lds, kval, qop, cop, g, r16, dstart);
+          __any(attend16_pass<HD, HALF, QB, MODE, DSTART, false>(k_lds, vt_lds, kval, ones_lds, qop, cop, g, r16,
+                                                                 dstart)),
+          0))
+    attend16_pass<HD, HALF, QB, MODE, DSTART, true>(k_lds, vt_lds, kval, ones_lds, qop, cop, g, r16, dstart);
 }
 
 }  // namespace split
@@ -822,8 +844,8 @@ template <int HD, int HALF, int P, int MASK>
 __device__ __forceinline__ void attend_pair(const Lds& L, const half8_t (&qop)[NB][OK], half8_t (&cop)[NB][KS], int g_in,
                                             int r16_in) {
   if constexpr (HD <= 16) {
-    split::attend16<HD, HALF, P, MASK, true>(L.k, L.vt, L.kval, qop[0], cop[0], g_in, r16_in);
-    split::attend16<HD, HALF, 7 - P, MASK, true>(L.k, L.vt, L.kval, qop[1], cop[1], g_in, r16_in);
+    split::attend16<HD, HALF, P, MASK, true>(L.k, L.vt, L.kval, L.ones, qop[0], cop[0], g_in, r16_in);
+    split::attend16<HD, HALF, 7 - P, MASK, true>(L.k, L.vt, L.kval, L.ones, qop[1], cop[1], g_in, r16_in);
   } else {
     int g = g_in, r16 = r16_in;  // opaque copies, as in attend16
     asm volatile("" : "+v"(g), "+v"(r16));
@@ -833,15 +855,15 @@ __device__ __forceinline__ void attend_pair(const Lds& L, const half8_t (&qop)[N
       for (int i = 0; i < 4; ++i) dstart[i] = 4 * g + i > r16 ? -INFINITY : 0.f;
     }
     const bool bad0 =
-        split::attend16_pass<HD, HALF, P, MASK, true, false>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16, dstart);
+        split::attend16_pass<HD, HALF, P, MASK, true, false>(L.k, L.vt, L.kval, L.ones, qop[0], cop[0], g, r16, dstart);
     const bool bad1 =
-        split::attend16_pass<HD, HALF, 7 - P, MASK, true, false>(L.k, L.vt, L.kval, qop[1], cop[1], g, r16, dstart);
+        split::attend16_pass<HD, HALF, 7 - P, MASK, true, false>(L.k, L.vt, L.kval, L.ones, qop[1], cop[1], g, r16, dstart);
     const bool redo0 = __any(bad0), redo1 = __any(bad1);
     if (__builtin_expect(redo0 || redo1, 0)) {  // unlikely, as in attend16
       if (redo0)
-        split::attend16_pass<HD, HALF, P, MASK, true, true>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16, dstart);
+        split::attend16_pass<HD, HALF, P, MASK, true, true>(L.k, L.vt, L.kval, L.ones, qop[0], cop[0], g, r16, dstart);
       if (redo1)
-        split::attend16_pass<HD, HALF, 7 - P, MASK, true, true>(L.k, L.vt, L.kval, qop[1], cop[1], g, r16, dstart);
+        split::attend16_pass<HD, HALF, 7 - P, MASK, true, true>(L.k, L.vt, L.kval, L.ones, qop[1], cop[1], g, r16, dstart);
     }
   }
 }
@@ -1122,14 +1144,14 @@ __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ 
     } else {
       constexpr bool SPLIT_DSTART = HD <= 16;
       switch (tb[0]) {
-        case 0: split::attend16<HD, HALF, 0, MASK, SPLIT_DSTART>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16); break;
-        case 1: split::attend16<HD, HALF, 1, MASK, SPLIT_DSTART>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16); break;
-        case 2: split::attend16<HD, HALF, 2, MASK, SPLIT_DSTART>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16); break;
-        case 3: split::attend16<HD, HALF, 3, MASK, SPLIT_DSTART>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16); break;
-        case 4: split::attend16<HD, HALF, 4, MASK, SPLIT_DSTART>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16); break;
-        case 5: split::attend16<HD, HALF, 5, MASK, SPLIT_DSTART>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16); break;
-        case 6: split::attend16<HD, HALF, 6, MASK, SPLIT_DSTART>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16); break;
-        default: split::attend16<HD, HALF, 7, MASK, SPLIT_DSTART>(L.k, L.vt, L.kval, qop[0], cop[0], g, r16); break;
+        case 0: split::attend16<HD, HALF, 0, MASK, SPLIT_DSTART>(L.k, L.vt, L.kval, L.ones, qop[0], cop[0], g, r16); break;
+        case 1: split::attend16<HD, HALF, 1, MASK, SPLIT_DSTART>(L.k, L.vt, L.kval, L.ones, qop[0], cop[0], g, r16); break;
+        case 2: split::attend16<HD, HALF, 2, MASK, SPLIT_DSTART>(L.k, L.vt, L.kval, L.ones, qop[0], cop[0], g, r16); break;
+        case 3: split::attend16<HD, HALF, 3, MASK, SPLIT_DSTART>(L.k, L.vt, L.kval, L.ones, qop[0], cop[0], g, r16); break;
+        case 4: split::attend16<HD, HALF, 4, MASK, SPLIT_DSTART>(L.k, L.vt, L.kval, L.ones, qop[0], cop[0], g, r16); break;
+        case 5: split::attend16<HD, HALF, 5, MASK, SPLIT_DSTART>(L.k, L.vt, L.kval, L.ones, qop[0], cop[0], g, r16); break;
+        case 6: split::attend16<HD, HALF, 6, MASK, SPLIT_DSTART>(L.k, L.vt, L.kval, L.ones, qop[0], cop[0], g, r16); break;
+        default: split::attend16<HD, HALF, 7, MASK, SPLIT_DSTART>(L.k, L.vt, L.kval, L.ones, qop[0], cop[0], g, r16); break;
       }
     }
     lds_barrier();  // every wave is done with K and V^T: their areas take exchanges now
@@ -1246,6 +1268,9 @@ __global__ __launch_bounds__(64 * NW, 1) void fused_stack8x2_kernel(
     for (int t = threadIdx.x; t < SMAX; t += 64 * NW)
       lds.kval[t] = t < S && (token_valid == nullptr || token_valid[(int64_t)blockIdx.x * S + t] != 0) ? 1 : 0;
   }
+  if constexpr (HD == 8) {
+    if (threadIdx.x < 128) lds.ones[threadIdx.x] = (half_t)1.0f;  // visible after the body's first barrier
+  }
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int pair = wave % 4;  // waves w and w + 4 (the two halves of blocks pair, 7 - pair) share a SIMD
   const SplitExchange none{nullptr, nullptr, nullptr, 0, 0, 0, 0u};
@@ -1279,6 +1304,9 @@ __global__ __launch_bounds__(64 * NW, 1) void fused_split_kernel(
   if constexpr (MASK != 0) {
     for (int t = threadIdx.x; t < SMAX; t += 64 * NW)
       lds.kval[t] = t < S && (token_valid == nullptr || token_valid[seq * S + t] != 0) ? 1 : 0;
+  }
+  if constexpr (HD == 8) {
+    if (threadIdx.x < 128) lds.ones[threadIdx.x] = (half_t)1.0f;  // visible after the body's first barrier
   }
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int pair = wave % 4;  // waves w and w + 4 share a SIMD (block assignment: stack8x2_body)
