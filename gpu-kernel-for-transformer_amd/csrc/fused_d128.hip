@@ -39,6 +39,7 @@
 // operations, so "vmcnt(0)" before a stage's barrier means exactly "this
 // stage has landed".
 #include "common.h"
+#include <type_traits>
 #include "../../include/xblock.h"
 
 namespace xb {
@@ -721,19 +722,51 @@ using split::Lds;
 using split::lds_barrier;
 
 // a[b][j] += staged-matrix output block (OB*half + j) times the operands of block b.
-template <bool SWAP, int NBT>
+// No weight copy to start from inside a product (the pair form starts it at
+// the group's barrier).
+struct NoCopy {};
+
+// a[b][j] += staged-matrix output block (OB*half + j) times the operands of
+// block b.  With a copy functor, the next matrix's copy is issued after the
+// first k-step's fragment reads rather than before them: the 32 KB queue at
+// the texture path (8 waves x 4 KB) stalls the waves that issue it last for
+// up to ~500 cycles, and the reads' latency then passes meanwhile.  The
+// split form does that (cfg4 -3 %, cfg1 -2 %); in the pair form it changed
+// nothing on cfg2 and cost 0.8 % with sixteen heads, so there the copy
+// stays at the barrier.
+template <bool SWAP, int NBT, typename Copy>
 __device__ __forceinline__ void stage_gemm2(const char* st, const half8_t (&act)[NBT][KS], float4_t (&a)[NBT][OB],
-                                            int half, int lane) {
+                                            int half, int lane, Copy&& copy) {
+  if constexpr (std::is_same_v<std::decay_t<Copy>, NoCopy>) {
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    half8_t f[OB];
+    for (int ks = 0; ks < KS; ++ks) {
+      half8_t f[OB];
 #pragma unroll
-    for (int j = 0; j < OB; ++j) f[j] = sfrag(st, (OB * half + j) * KS + ks, lane);
+      for (int j = 0; j < OB; ++j) f[j] = sfrag(st, (OB * half + j) * KS + ks, lane);
 #pragma unroll
-    for (int b = 0; b < NBT; ++b)
+      for (int b = 0; b < NBT; ++b)
 #pragma unroll
-      for (int j = 0; j < OB; ++j)
-        a[b][j] = SWAP ? mfma16x16x32(f[j], act[b][ks], a[b][j]) : mfma16x16x32(act[b][ks], f[j], a[b][j]);
+        for (int j = 0; j < OB; ++j)
+          a[b][j] = SWAP ? mfma16x16x32(f[j], act[b][ks], a[b][j]) : mfma16x16x32(act[b][ks], f[j], a[b][j]);
+    }
+  } else {
+    half8_t f[2][OB];
+#pragma unroll
+    for (int j = 0; j < OB; ++j) f[0][j] = sfrag(st, (OB * half + j) * KS, lane);
+    copy();
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      if (ks + 1 < KS) {
+#pragma unroll
+        for (int j = 0; j < OB; ++j) f[(ks + 1) & 1][j] = sfrag(st, (OB * half + j) * KS + ks + 1, lane);
+      }
+#pragma unroll
+      for (int b = 0; b < NBT; ++b)
+#pragma unroll
+        for (int j = 0; j < OB; ++j)
+          a[b][j] = SWAP ? mfma16x16x32(f[ks & 1][j], act[b][ks], a[b][j])
+                         : mfma16x16x32(act[b][ks], f[ks & 1][j], a[b][j]);
+    }
   }
 }
 
@@ -1035,10 +1068,25 @@ __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ 
       }
     }
   };
+  // Start of group gi: its loads (issued during group gi-1) have landed and
+  // every wave is done with group gi-1's stage, which now receives gi+1: at
+  // once in the pair form, from inside gi's product in the split form
+  // (copy_next, see stage_gemm2).
   auto begin_group = [&](int gi) -> const char* {
     drain_and_barrier();
-    if (gi + 1 < groups) issue_group(gi + 1);
+    if constexpr (!SPLIT) {
+      if (gi + 1 < groups) issue_group(gi + 1);
+    }
     return wst[gi & 1];
+  };
+  auto copy_next = [&](int gi) {
+    if constexpr (SPLIT) {
+      return [&, gi]() {
+        if (gi + 1 < groups) issue_group(gi + 1);
+      };
+    } else {
+      return NoCopy{};
+    }
   };
 
   // Residual stream, own half of both blocks: res[b][j][i] = x[16 tb[b] + r16][16 (OB half + j) + 4 g + i].
@@ -1074,7 +1122,7 @@ __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ 
       for (int b = 0; b < NBT; ++b)
 #pragma unroll
         for (int j = 0; j < OB; ++j) a[b][j] = ld4(pp + P_BK + 16 * (OB * half + j) + 4 * g);
-      stage_gemm2<true>(st, xn, a, half, lane);
+      stage_gemm2<true>(st, xn, a, half, lane, copy_next(g0 + 0));
 #pragma unroll
       for (int b = 0; b < NBT; ++b)
 #pragma unroll
@@ -1096,7 +1144,7 @@ __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ 
 #pragma unroll
         for (int b = 0; b < NBT; ++b) a[b][j] = float4_t{bv, bv, bv, bv};
       }
-      stage_gemm2<false>(st, xn, a, half, lane);
+      stage_gemm2<false>(st, xn, a, half, lane, copy_next(g0 + 1));
 #pragma unroll
       for (int b = 0; b < NBT; ++b)
 #pragma unroll
@@ -1118,7 +1166,7 @@ __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ 
       for (int b = 0; b < NBT; ++b)
 #pragma unroll
         for (int j = 0; j < OB; ++j) qc[b][j] = ld4(pp + P_BQ + 16 * (OB * half + j) + 4 * g);
-      stage_gemm2<true>(st, xn, qc, half, lane);
+      stage_gemm2<true>(st, xn, qc, half, lane, copy_next(g0 + 2));
 #pragma unroll
       for (int b = 0; b < NBT; ++b)
 #pragma unroll
@@ -1173,7 +1221,7 @@ __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ 
       for (int b = 0; b < NBT; ++b)
 #pragma unroll
         for (int j = 0; j < OB; ++j) a[b][j] = ld4(pp + P_BO + 16 * (OB * half + j) + 4 * g);
-      stage_gemm2<true>(st, cop, a, half, lane);
+      stage_gemm2<true>(st, cop, a, half, lane, copy_next(g0 + 3));
 #pragma unroll
       for (int b = 0; b < NBT; ++b)
 #pragma unroll
@@ -1196,7 +1244,7 @@ __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ 
       for (int b = 0; b < NBT; ++b)
 #pragma unroll
         for (int j = 0; j < OB; ++j) a[b][j] = ld4(pp + P_B1 + 16 * (OB * half + j) + 4 * g);
-      stage_gemm2<true>(st, xn, a, half, lane);
+      stage_gemm2<true>(st, xn, a, half, lane, copy_next(g0 + 4));
       half8_t own[NBT][OK];
 #pragma unroll
       for (int b = 0; b < NBT; ++b)
@@ -1214,7 +1262,7 @@ __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ 
       for (int b = 0; b < NBT; ++b)
 #pragma unroll
         for (int j = 0; j < OB; ++j) a[b][j] = ld4(pp + P_B2 + 16 * (OB * half + j) + 4 * g);
-      stage_gemm2<true>(st, hf, a, half, lane);
+      stage_gemm2<true>(st, hf, a, half, lane, copy_next(g0 + 5));
 #pragma unroll
       for (int b = 0; b < NBT; ++b)
 #pragma unroll
