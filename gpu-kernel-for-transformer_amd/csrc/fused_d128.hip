@@ -39,7 +39,6 @@
 // operations, so "vmcnt(0)" before a stage's barrier means exactly "this
 // stage has landed".
 #include "common.h"
-#include <type_traits>
 #include "../../include/xblock.h"
 
 namespace xb {
@@ -722,51 +721,33 @@ using split::Lds;
 using split::lds_barrier;
 
 // a[b][j] += staged-matrix output block (OB*half + j) times the operands of block b.
-// No weight copy to start from inside a product (the pair form starts it at
-// the group's barrier).
-struct NoCopy {};
-
 // a[b][j] += staged-matrix output block (OB*half + j) times the operands of
-// block b.  With a copy functor, the next matrix's copy is issued after the
-// first k-step's fragment reads rather than before them: the 32 KB queue at
-// the texture path (8 waves x 4 KB) stalls the waves that issue it last for
-// up to ~500 cycles, and the reads' latency then passes meanwhile.  The
-// split form does that (cfg4 -3 %, cfg1 -2 %); in the pair form it changed
-// nothing on cfg2 and cost 0.8 % with sixteen heads, so there the copy
-// stays at the barrier.
+// block b, with each k-step's fragments read one step ahead.  copy() issues
+// the next matrix's weight copy after the first k-step's products: the
+// 32 KB it queues at the texture path (8 waves x 4 KB) stalls the waves
+// that issue it last for up to ~500 cycles, and with the products queued
+// first the matrix cores work through that stall instead of waiting behind
+// it.  (Issued at the group's barrier, before the first fragment reads, it
+// cost cfg2 0.8 % and cfg1 2 %.)
 template <bool SWAP, int NBT, typename Copy>
 __device__ __forceinline__ void stage_gemm2(const char* st, const half8_t (&act)[NBT][KS], float4_t (&a)[NBT][OB],
                                             int half, int lane, Copy&& copy) {
-  if constexpr (std::is_same_v<std::decay_t<Copy>, NoCopy>) {
+  half8_t f[2][OB];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      half8_t f[OB];
+  for (int j = 0; j < OB; ++j) f[0][j] = sfrag(st, (OB * half + j) * KS, lane);
 #pragma unroll
-      for (int j = 0; j < OB; ++j) f[j] = sfrag(st, (OB * half + j) * KS + ks, lane);
+  for (int ks = 0; ks < KS; ++ks) {
+    if (ks + 1 < KS) {
 #pragma unroll
-      for (int b = 0; b < NBT; ++b)
-#pragma unroll
-        for (int j = 0; j < OB; ++j)
-          a[b][j] = SWAP ? mfma16x16x32(f[j], act[b][ks], a[b][j]) : mfma16x16x32(act[b][ks], f[j], a[b][j]);
+      for (int j = 0; j < OB; ++j) f[(ks + 1) & 1][j] = sfrag(st, (OB * half + j) * KS + ks + 1, lane);
     }
-  } else {
-    half8_t f[2][OB];
 #pragma unroll
-    for (int j = 0; j < OB; ++j) f[0][j] = sfrag(st, (OB * half + j) * KS, lane);
-    copy();
+    for (int b = 0; b < NBT; ++b)
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      if (ks + 1 < KS) {
-#pragma unroll
-        for (int j = 0; j < OB; ++j) f[(ks + 1) & 1][j] = sfrag(st, (OB * half + j) * KS + ks + 1, lane);
-      }
-#pragma unroll
-      for (int b = 0; b < NBT; ++b)
-#pragma unroll
-        for (int j = 0; j < OB; ++j)
-          a[b][j] = SWAP ? mfma16x16x32(f[ks & 1][j], act[b][ks], a[b][j])
-                         : mfma16x16x32(act[b][ks], f[ks & 1][j], a[b][j]);
-    }
+      for (int j = 0; j < OB; ++j)
+        a[b][j] = SWAP ? mfma16x16x32(f[ks & 1][j], act[b][ks], a[b][j])
+                       : mfma16x16x32(act[b][ks], f[ks & 1][j], a[b][j]);
+    if (ks == 0) copy();
   }
 }
 
@@ -1069,24 +1050,16 @@ __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ 
     }
   };
   // Start of group gi: its loads (issued during group gi-1) have landed and
-  // every wave is done with group gi-1's stage, which now receives gi+1: at
-  // once in the pair form, from inside gi's product in the split form
-  // (copy_next, see stage_gemm2).
+  // every wave is done with group gi-1's stage, which receives gi+1 from
+  // inside gi's product (copy_next, see stage_gemm2).
   auto begin_group = [&](int gi) -> const char* {
     drain_and_barrier();
-    if constexpr (!SPLIT) {
-      if (gi + 1 < groups) issue_group(gi + 1);
-    }
     return wst[gi & 1];
   };
   auto copy_next = [&](int gi) {
-    if constexpr (SPLIT) {
-      return [&, gi]() {
-        if (gi + 1 < groups) issue_group(gi + 1);
-      };
-    } else {
-      return NoCopy{};
-    }
+    return [&, gi]() {
+      if (gi + 1 < groups) issue_group(gi + 1);
+    };
   };
 
   // Residual stream, own half of both blocks: res[b][j][i] = x[16 tb[b] + r16][16 (OB half + j) + 4 g + i].
