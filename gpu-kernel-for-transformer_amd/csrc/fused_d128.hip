@@ -1062,7 +1062,16 @@ __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ 
     };
   };
 
-  // Residual stream, own half of both blocks: res[b][j][i] = x[16 tb[b] + r16][16 (OB half + j) + 4 g + i].
+  // Layer 0's vectors, then the residual stream (own half of both blocks:
+  // res[b][j][i] = x[16 tb[b] + r16][16 (OB half + j) + 4 g + i]), then the
+  // first matrix's copy.  Loads retire in issue order, so in the pair form,
+  // once at most this wave's four copy loads are outstanding, the vectors
+  // and rows have landed: LayerNorm 1 then runs while the copy arrives (it
+  // is waited for at the K group's barrier; cfg2 -0.4 %).  The split form
+  // waits for all of it, issued rows first (the overlap cost cfg4 1-2 %).
+  if constexpr (!SPLIT) {
+    if (lane < 40) dma16(ppack + wave * 160 + lane * 4, prm[0] + wave * 160);
+  }
   float4_t res[NBT][OB];
 #pragma unroll
   for (int b = 0; b < NBT; ++b) {
@@ -1071,9 +1080,19 @@ __device__ __forceinline__ void stack8x2_body(Lds& L, const float* __restrict__ 
     for (int j = 0; j < OB; ++j)
       res[b][j] = tok < S ? ld4(xs + (int64_t)tok * D + 16 * (OB * half + j) + 4 * g) : float4_t{0.f, 0.f, 0.f, 0.f};
   }
-  if (lane < 40) dma16(ppack + wave * 160 + lane * 4, prm[0] + wave * 160);
+  if constexpr (SPLIT) {
+    if (lane < 40) dma16(ppack + wave * 160 + lane * 4, prm[0] + wave * 160);
+  }
   issue_group(0);
-  drain_and_barrier();
+  if constexpr (SPLIT) {
+    drain_and_barrier();
+  } else {
+    static_assert(MAT_FRAGS / NW == 4, "four copy loads per wave");
+    __builtin_amdgcn_s_waitcnt(4 | (7 << 4) | (0 << 8) | (0 << 14));  // vmcnt(4) expcnt(7) lgkmcnt(0)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  }
 
   for (int layer = 0; layer < layers; ++layer) {
     const float* pp = prm[layer & 1];
