@@ -720,7 +720,6 @@ using split::xslot;
 using split::Lds;
 using split::lds_barrier;
 
-// a[b][j] += staged-matrix output block (OB*half + j) times the operands of block b.
 // a[b][j] += staged-matrix output block (OB*half + j) times the operands of
 // block b, with each k-step's fragments read one step ahead.  copy() issues
 // the next matrix's weight copy after the first k-step's products: the
