@@ -659,6 +659,12 @@ def _new_split_workspace(device: torch.device, seq_len: int, num_heads: int, num
     return torch.zeros(max(size, need), device=device, dtype=torch.uint8)
 
 
+@lru_cache(maxsize=256)
+def _split_workspace_bytes(batch: int, seq_len: int, num_heads: int, num_layers: int, causal: bool) -> int:
+    """xb_fused_forward_d128_workspace_bytes, a function of the shape alone (0: one workgroup per sequence)."""
+    return int(lib().xb_fused_forward_d128_workspace_bytes(batch, seq_len, num_heads, num_layers, int(causal)))
+
+
 def fused_split_workspace(device, batch: int, seq_len: int, num_heads: int, num_layers: int,
                           causal: bool) -> Optional[torch.Tensor]:
     """The zero-filled uint8 workspace xb_fused_forward_d128_ws needs for this shape.
@@ -674,8 +680,7 @@ def fused_split_workspace(device, batch: int, seq_len: int, num_heads: int, num_
     could overlap eager calls that share it): the call then runs the
     one-workgroup form, with the same results.
     """
-    need = int(lib().xb_fused_forward_d128_workspace_bytes(
-        int(batch), int(seq_len), int(num_heads), int(num_layers), int(bool(causal))))
+    need = _split_workspace_bytes(int(batch), int(seq_len), int(num_heads), int(num_layers), bool(causal))
     if need <= 0:
         return None
     device = torch.device(device)

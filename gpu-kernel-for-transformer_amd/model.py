@@ -40,6 +40,7 @@ reference (TTB:503-508) there is no sequence-length limit: the key mask is a
 from __future__ import annotations
 
 import dataclasses
+import operator
 from typing import Dict, Optional, Tuple
 
 import torch
@@ -85,6 +86,9 @@ class TransformerBlockParameters(nn.Module):
 
     def forward(self, *args, **kwargs):  # pragma: no cover - explicit guard
         raise RuntimeError("run blocks through UserOptimizedTransformer.forward")
+
+
+_VERSION_OF = operator.attrgetter("_version")  # raises RuntimeError on inference tensors, as _version does
 
 
 def _tensor_version(tensor: torch.Tensor) -> Optional[int]:
@@ -287,13 +291,19 @@ class UserOptimizedTransformer(nn.Module):
         """Conditions of the whole-stack kernel beyond the shape: the toggle, LayerNorm eps 1e-5 with affine."""
         if not self._fused_stack_enabled:
             return False
-        return all(n.eps == 1e-5 and n.weight is not None and n.bias is not None for n in self._tree()[1])
+        # Parameters read from each module's registry directly: going through
+        # nn.Module.__getattr__ for 18 of them cost microseconds per forward.
+        for norm in self._tree()[1]:
+            registered = norm._parameters
+            if norm.eps != 1e-5 or registered.get("weight") is None or registered.get("bias") is None:
+                return False
+        return True
 
     def _fused_stack_parameters(self) -> Tuple[torch.Tensor, torch.Tensor, int]:
         """Fragment-packed FP16 weights, FP32 bias/LayerNorm buffer and LayerNorm affine mask, cached by version."""
         params = self._tree()[0]
         try:
-            key = (tuple([p._version for p in params]), tuple([p.data_ptr() for p in params]))
+            key = (tuple(map(_VERSION_OF, params)), tuple(map(torch.Tensor.data_ptr, params)))
         except RuntimeError:  # inference-mode parameters have no version counter: never reuse
             key = None
         cached = self.__dict__.get("_fused_stack_cache")
@@ -414,7 +424,8 @@ class UserOptimizedTransformer(nn.Module):
                 raise ValueError("KV-cached decoding does not support padding")
             with torch.no_grad():
                 return self._forward_hip_cached(x)
-        chunk = self._chunk_size(x.shape[0], x.shape[1])
+        plan = self.execution_plan(x.shape[0], x.shape[1])
+        chunk = self._large_batch_chunk_size or plan.batch_chunk_size  # as _chunk_size
         with torch.no_grad():
             if chunk and x.shape[0] > chunk:
                 output = torch.empty_like(x)
@@ -423,17 +434,21 @@ class UserOptimizedTransformer(nn.Module):
                     self._forward_hip(x[start:end], out=output[start:end],
                                       token_valid=None if token_valid is None else token_valid[start:end])
                 return output
-            return self._forward_hip(x, token_valid=token_valid)
+            # An unpadded whole batch runs the plan just looked up.
+            return self._forward_hip(x, token_valid=token_valid, plan=plan if token_valid is None else None)
 
     def _forward_hip(self, x: torch.Tensor, out: Optional[torch.Tensor] = None,
-                     token_valid: Optional[torch.Tensor] = None) -> torch.Tensor:
+                     token_valid: Optional[torch.Tensor] = None,
+                     plan: Optional[ShapeExecutionPlan] = None) -> torch.Tensor:
         """The fused kernel sequence of TTB:1092-1148 for one batch.
 
         token_valid: None (every token valid) or a contiguous [B, S] uint8 mask
-        with at least one zero.
+        with at least one zero.  plan: execution_plan(B, S, padded=token_valid
+        is not None) when the caller already has it.
         """
         cfg = self.config
-        plan = self.execution_plan(x.shape[0], x.shape[1], padded=token_valid is not None)
+        if plan is None:
+            plan = self.execution_plan(x.shape[0], x.shape[1], padded=token_valid is not None)
         if not plan.runnable:
             raise ValueError(f"no gfx950 kernel sequence for this input: {plan.forward_strategy}")
         if plan.fused:
