@@ -165,6 +165,23 @@ def test_tree_cache_follows_registrations(pkg):
     assert not model.execution_plan(2, 8).fused
 
 
+def test_fused_eligibility_checks_every_layer_norm_on_each_call(pkg):
+    """The whole-stack kernel needs eps 1e-5, a weight and a bias on every LayerNorm, re-read per call."""
+    model = pkg.UserOptimizedTransformer(pkg.TransformerConfig(2, 8, 128, 4, 128, 2, True)).eval()
+    assert model._fused_stack_eligible() and model.execution_plan(2, 8).fused
+    model.layers[0].norm2.eps = 1e-6                       # a plain attribute: no registration hook fires
+    assert not model._fused_stack_eligible() and not model.execution_plan(2, 8).fused
+    model.layers[0].norm2.eps = 1e-5
+    assert model._fused_stack_eligible() and model.execution_plan(2, 8).fused
+    for replacement in (torch.nn.LayerNorm(128, elementwise_affine=False), torch.nn.LayerNorm(128, bias=False)):
+        model.layers[1].norm1 = replacement                # weight or bias registered as None
+        assert not model._fused_stack_eligible()
+    model.layers[1].norm1 = torch.nn.LayerNorm(128)
+    assert model._fused_stack_eligible()
+    model.enable_fused_stack(False)
+    assert not model._fused_stack_eligible() and not model.execution_plan(2, 8).fused
+
+
 def test_product_never_touches_the_oracle():
     for path in (REPO / "gpu-kernel-for-transformer_amd").rglob("*.py"):
         text = path.read_text()
