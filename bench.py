@@ -799,7 +799,8 @@ def run_config(args, pkg, config, shape_id, name, is_head, build, make_input, ti
     else:
         del out
     if shape_id == 6 and not args.profile_only and not args.batch:
-        # The reference's own shape-6 form: chunks of 1024 with a hipGraph per chunk shape.
+        # The reference's own shape-6 form: chunks of 1024 with graphs requested (a chunk whose
+        # forward is one kernel is launched eagerly into its output slice instead of replayed).
         chunked = chunking.BatchChunkedTransformer(model, 1024, all_tokens_valid=True, use_cuda_graphs=True)
         with torch.inference_mode():
             c_ms, _ = time_steps(lambda: chunked(x), 10, 2)
@@ -807,7 +808,7 @@ def run_config(args, pkg, config, shape_id, name, is_head, build, make_input, ti
         entry_["reference_form_chunk1024_graphs"] = {
             "ms": c_ms, "tokens_per_s": tokens / (c_ms / 1e3), "equal_to_unchunked": same,
             "status": chunked.graph_status}
-        log(f"[bench] {name}: chunk-1024 per-chunk graphs {c_ms:.3f} ms ({chunked.graph_status}); bitwise equal: {same}")
+        log(f"[bench] {name}: chunk-1024 form {c_ms:.3f} ms ({chunked.graph_status}); bitwise equal: {same}")
         del chunked
     del baseline, model, x
     return entry_, head_extra

@@ -394,6 +394,19 @@ class UserOptimizedTransformer(nn.Module):
 
     # ----------------------------------------------------------------- forward
     def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+        return self._forward_impl(x, valid_token_mask, None)
+
+    def _forward_into(self, x: torch.Tensor, out: torch.Tensor,
+                      valid_token_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """forward(x, valid_token_mask) written into `out` (contiguous float32, x's shape) and returned.
+
+        BatchChunkedTransformer writes each chunk into its slice of the batch
+        output this way, with no copy of a separately allocated result.
+        """
+        return self._forward_impl(x, valid_token_mask, out)
+
+    def _forward_impl(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor],
+                      out: Optional[torch.Tensor]) -> torch.Tensor:
         if x.device.type != "cuda":
             raise RuntimeError(
                 "UserOptimizedTransformer runs only on the gfx950 HIP path; move the model and "
@@ -407,6 +420,9 @@ class UserOptimizedTransformer(nn.Module):
             raise ValueError("the gfx950 path expects a float32 residual stream input")
         if self.training:
             raise RuntimeError("UserOptimizedTransformer is inference-only; call eval()")
+        if out is not None and (tuple(out.shape) != tuple(x.shape) or out.dtype != torch.float32
+                                or out.device != x.device or not out.is_contiguous()):
+            raise ValueError(f"out must be a contiguous float32 tensor of shape {tuple(x.shape)} on {x.device}")
         token_valid = None
         if valid_token_mask is not None:
             if tuple(valid_token_mask.shape) != tuple(x.shape[:2]):
@@ -423,19 +439,20 @@ class UserOptimizedTransformer(nn.Module):
             if token_valid is not None:
                 raise ValueError("KV-cached decoding does not support padding")
             with torch.no_grad():
-                return self._forward_hip_cached(x)
+                result = self._forward_hip_cached(x)
+            return result if out is None else out.copy_(result)
         plan = self.execution_plan(x.shape[0], x.shape[1])
         chunk = self._large_batch_chunk_size or plan.batch_chunk_size  # as _chunk_size
         with torch.no_grad():
             if chunk and x.shape[0] > chunk:
-                output = torch.empty_like(x)
+                output = torch.empty_like(x) if out is None else out
                 for start in range(0, x.shape[0], chunk):
                     end = min(start + chunk, x.shape[0])
                     self._forward_hip(x[start:end], out=output[start:end],
                                       token_valid=None if token_valid is None else token_valid[start:end])
                 return output
             # An unpadded whole batch runs the plan just looked up.
-            return self._forward_hip(x, token_valid=token_valid, plan=plan if token_valid is None else None)
+            return self._forward_hip(x, out=out, token_valid=token_valid, plan=plan if token_valid is None else None)
 
     def _forward_hip(self, x: torch.Tensor, out: Optional[torch.Tensor] = None,
                      token_valid: Optional[torch.Tensor] = None,

@@ -143,9 +143,10 @@ def test_maybe_cuda_graph_refuses_a_failed_handoff(pkg, cuda, monkeypatch):
 
 
 def test_batch_chunked_graphs_match_whole_batch(pkg, cuda):
-    """Per-chunk-shape graphs (full chunk and remainder) over static buffers, split and
-    one-workgroup whole-stack forms, plus a per-op geometry: bitwise equal to the
-    whole-batch forward on two different inputs."""
+    """Chunks of the split and one-workgroup whole-stack forms (one kernel each: launched
+    eagerly into the output, no graph) and of a per-op geometry (per-chunk-shape graphs
+    over static buffers, full chunk and remainder): bitwise equal to the whole-batch
+    forward on two different inputs."""
     _, chunks, _ = _runners(pkg)
     for geom, chunk in (((45, 128, 128, 4, 128, 2), 16), ((300, 128, 128, 4, 128, 2), 128),
                         ((9, 96, 256, 4, 256, 2), 4)):
@@ -160,8 +161,12 @@ def test_batch_chunked_graphs_match_whole_batch(pkg, cuda):
                 out = runner(x)
             torch.cuda.synchronize()
             assert torch.equal(out, whole), f"{geom} chunk {chunk} seed {seed}"
-        expected_graphs = 1 + int(config.batch_size % chunk != 0)
-        assert runner.graph_status == f"one hipGraph per chunk shape ({expected_graphs} captured)", runner.graph_status
+        if optimized.execution_plan(chunk, config.seq_len).fused:
+            assert not runner._graphs, geom
+            assert runner.graph_status.startswith("one-kernel chunk forwards: launched eagerly"), runner.graph_status
+        else:
+            expected_graphs = 1 + int(config.batch_size % chunk != 0)
+            assert runner.graph_status == f"one hipGraph per chunk shape ({expected_graphs} captured)", runner.graph_status
 
 
 def test_batch_chunked_padded_and_eager(pkg, cuda):
@@ -178,9 +183,31 @@ def test_batch_chunked_padded_and_eager(pkg, cuda):
         assert torch.equal(runner(x, mask), optimized(x, mask))
 
 
+def test_forward_into_writes_the_given_buffer(pkg, cuda):
+    """The chunk runner's direct path: _forward_into returns `out` itself, bitwise equal to
+    forward, for a whole-stack, a per-op and a padded input; a wrong buffer is refused."""
+    for geom in ((6, 128, 128, 4, 128, 2), (3, 96, 256, 4, 256, 2)):
+        config = pkg.TransformerConfig(*geom, True)
+        _, optimized = _models(pkg, config, cuda)
+        x = torch.randn(config.batch_size, config.seq_len, config.d_model, device=cuda)
+        mask = torch.ones(config.batch_size, config.seq_len, device=cuda, dtype=torch.bool)
+        mask[1, config.seq_len // 2:] = False
+        for m in (None, mask):
+            out = torch.empty_like(x)
+            with torch.inference_mode():
+                got = optimized._forward_into(x, out, m)
+                expected = optimized(x, m)
+            assert got is out and torch.equal(out, expected), (geom, m is None)
+        with pytest.raises(ValueError, match="out must be"):
+            optimized._forward_into(x, torch.empty(x.shape, device=cuda, dtype=torch.float16))
+        with pytest.raises(ValueError, match="out must be"):
+            optimized._forward_into(x, torch.empty(x.shape[0] + 1, *x.shape[1:], device=cuda))
+
+
 def test_shape6_chunk_1024_graphs_against_oracle(pkg, cuda):
-    """The reference's shape-6 configuration: B=10000 in chunks of 1024 with per-chunk graphs,
-    equal to the whole batch bitwise, and slices of it against the CPU oracle."""
+    """The reference's shape-6 configuration: B=10000 in chunks of 1024 with graphs requested
+    (each chunk is one whole-stack launch, so it writes its output slice eagerly), equal to
+    the whole batch bitwise, and slices of it against the CPU oracle."""
     _, chunks, _ = _runners(pkg)
     config = pkg.OFFICIAL_BENCHMARK_SHAPES[6]
     baseline, optimized = _models(pkg, config, cuda)
@@ -191,6 +218,7 @@ def test_shape6_chunk_1024_graphs_against_oracle(pkg, cuda):
         out = runner(x)
         whole = optimized(x)
     assert torch.equal(out, whole)
+    assert runner.graph_status.startswith("one-kernel chunk forwards"), runner.graph_status
     for start in (0, 9216, 9984):  # first chunk, the remainder chunk, its last rows
         rows = slice(start, start + 16)
         with torch.inference_mode():
