@@ -134,7 +134,7 @@ class BatchChunkedTransformer(nn.Module):
             chunk = x[start:end]
             chunk_mask = None if mask is None else mask[start:end]
             graph = None
-            if self.use_cuda_graphs and not self._one_launch(chunk):
+            if self.use_cuda_graphs and chunk.numel() and not self._one_launch(chunk):
                 graph = self._graph_for(chunk)
             if graph is not None:
                 graph.run_into(chunk, output[start:end])

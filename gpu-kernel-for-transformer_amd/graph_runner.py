@@ -132,6 +132,8 @@ def _why_not_graphed(model: nn.Module, x: torch.Tensor, valid_token_mask: Option
         return "graphs require a GPU input"
     if bool(getattr(model, "_kv_cache_enabled", False)):
         return "stateful KV-cache decoding uses the eager path"
+    if x.numel() == 0:
+        return "empty input: nothing to launch"
     single_launch = getattr(model, "_single_launch_forward", None)
     if single_launch is not None and single_launch(x, valid_token_mask):
         return "one-kernel forward: launched eagerly (a replay adds only the output copy)"

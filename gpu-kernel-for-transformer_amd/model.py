@@ -432,8 +432,10 @@ class UserOptimizedTransformer(nn.Module):
                 raise ValueError("valid_token_mask must be on the input's device")
             if valid_token_mask.dtype not in (torch.bool, torch.uint8):
                 raise ValueError("valid_token_mask must be bool or uint8")
-            if not self._all_tokens_valid(valid_token_mask, x.shape[1]):
+            if x.numel() and not self._all_tokens_valid(valid_token_mask, x.shape[1]):
                 token_valid = (valid_token_mask != 0).to(torch.uint8).contiguous()
+        if x.numel() == 0:  # no sequence or no token: an empty result, nothing launched, no cache change
+            return torch.empty_like(x) if out is None else out
         x = x.contiguous()
         if self._kv_cache_enabled:
             if token_valid is not None:

@@ -377,6 +377,29 @@ def test_mask_argument_errors(pkg, cuda):
         optimized(x, torch.ones(2, 8, dtype=torch.float32, device=cuda))
 
 
+@pytest.mark.parametrize("d_model", [128, 256])
+def test_empty_batch_or_sequence(pkg, cuda, d_model):
+    """No sequence (B = 0) or no token (S = 0): an empty float32 result of the input's shape,
+    as the reference's PyTorch ops give, with or without a mask, and through graph replay
+    and batch chunking."""
+    config = pkg.TransformerConfig(2, 64, d_model, 4, d_model, 2, True)
+    _, optimized = _models(pkg, config, cuda)
+    graphs = __import__(pkg.__name__ + ".graph_runner", fromlist=["maybe_cuda_graph"])
+    chunks = __import__(pkg.__name__ + ".batch_chunk_runner", fromlist=["BatchChunkedTransformer"])
+    for b, s in ((0, 64), (2, 0), (0, 0)):
+        x = torch.randn(b, s, d_model, device=cuda)
+        mask = torch.ones(b, s, dtype=torch.bool, device=cuda)
+        with torch.inference_mode():
+            results = [optimized(x), optimized(x, mask), optimized(x, mask == 0)]
+            runner, graphed, reason = graphs.maybe_cuda_graph(optimized, x, None, enabled=True)
+            assert runner is optimized and not graphed and reason.startswith("empty input"), reason
+            results.append(runner(x))
+            results.append(chunks.BatchChunkedTransformer(optimized, 16, all_tokens_valid=True, use_cuda_graphs=True)(x))
+        torch.cuda.synchronize()
+        for y in results:
+            assert y.shape == x.shape and y.dtype == torch.float32 and y.device == x.device, (b, s)
+
+
 # ----------------------------------------------------------------------------- KV-cached decoding
 @pytest.mark.parametrize(
     "geom,pieces",
