@@ -66,6 +66,27 @@ def test_fused_residual_layer_norm(pkg, cuda, cols, upd_dtype, mode):
         torch.testing.assert_close(norm.cpu(), ref, atol=2e-5, rtol=2e-5)
 
 
+def test_stream_handle_is_the_current_stream(pkg, cuda):
+    """Launches go to torch's current stream: the raw handle equals current_stream().cuda_stream
+    on the default stream, on a side stream and under graph capture."""
+    capi = pkg._capi
+    assert capi.stream_handle(cuda) == torch.cuda.current_stream(cuda).cuda_stream
+    side = torch.cuda.Stream(device=cuda)
+    with torch.cuda.stream(side):
+        assert capi.stream_handle(cuda) == side.cuda_stream != torch.cuda.default_stream(cuda).cuda_stream
+        assert capi.stream_handle(None) == side.cuda_stream
+    graph = torch.cuda.CUDAGraph()
+    x = torch.zeros(4, device=cuda)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph, stream=side):
+        handle = capi.stream_handle(cuda)
+        x += 1  # something to capture
+    assert handle == side.cuda_stream
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(x, torch.ones(4, device=cuda))
+
+
 def test_layer_norm_errors(pkg, cuda):
     x = torch.randn(4, 128, device=cuda)
     with pytest.raises(ValueError):
