@@ -373,7 +373,8 @@ def main(argv=None) -> int:
     args = parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X only: this build has no multi-GPU path "
-              "(the batch shards with no exchange step; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "(sequences are independent, so the batch would shard across GPUs with no exchange step). "
+              "Run with --gpus 1.", file=sys.stderr)
         return 2
 
     import torch
