@@ -1,8 +1,8 @@
 #!/usr/bin/env python3
 """Throughput of the MI355X causal pre-norm block inference path.
 
-Headline workload (the BASELINE metric's config that fits one GPU):
-BASELINE config 2 = official shape 6, B=10000 S=128 D=128 H=4 F=128 L=4, one
+Headline workload (the benchmark metric's configuration that fits one GPU):
+benchmark config 2 = official shape 6, B=10000 S=128 D=128 H=4 F=128 L=4, one
 "step" = one full forward of the whole batch with the input resident in HBM.
 Weights: nn.Linear default init under torch.manual_seed(1234) (random, no
 checkpoint); input: x ~ N(0,1) from seed 1234+100000 (synthetic), as the
@@ -27,10 +27,11 @@ Printed as ONE JSON line with, besides the driver's fields:
                   sequences for cfg2 and cfg5); every config's whole output
                   must also be finite (streamed_shape14.py:167-169) and no
                   split-form K/V hand-off may have failed
-  per_config      all five BASELINE configs: tokens/s, ms, execution plan,
+  per_config      all five benchmark configs: tokens/s, ms, execution plan,
                   dominant-kernel roofline, forward roofline, accuracy; cfg2
                   also times the reference's own shape-6 form (chunks of 1024
-                  with a hipGraph per chunk shape, TTB:1740, :1826-1846)
+                  with graphs requested, TTB:1740, :1826-1846; each chunk is
+                  one whole-stack launch, written into the output eagerly)
   decode          KV-cached single-token steps at cfg5's geometry
 Timed call: forward(x, all-True mask), the reference harness's (TTB:1478-1491);
 each config also reports the reference harness's per-call statistics
@@ -82,7 +83,7 @@ def parse_args(argv=None):
     p.add_argument("--steps", type=int, default=100)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--workload", type=int, default=6, choices=range(1, 15), metavar="SHAPE_ID",
-                   help="official shape id (1-14) of the headline line; default 6 = BASELINE config 2")
+                   help="official shape id (1-14) of the headline line; default 6 = benchmark config 2")
     p.add_argument("--no-per-config", action="store_true", help="skip the other four configs")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="bound on the CPU baseline's timed work")
     p.add_argument("--no-cpu-baseline", action="store_true")

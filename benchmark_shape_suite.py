@@ -75,7 +75,7 @@ class CaseResult:
 
 
 def parse_case_ids(specification: str, known: Sequence[int], configs: Sequence[int]) -> List[int]:
-    """``all``, ``configs`` (the five BASELINE configs), or values such as ``1,3,7`` / ``1-5,12``.
+    """``all``, ``configs`` (the five benchmark configs), or values such as ``1,3,7`` / ``1-5,12``.
 
     Same grammar and errors as the reference (benchmark_shape_suite.py:34-56).
     """
@@ -289,7 +289,7 @@ def run_suite(shape_ids: Sequence[int], shapes: Dict, args: argparse.Namespace, 
 def parse_args(argv: Optional[Sequence[str]] = None) -> argparse.Namespace:
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--cases", default="configs",
-                   help="all, configs (the five BASELINE configs: shapes 1,6,8,11,14), or ids such as 1,3,7 or 1-5,12")
+                   help="all, configs (the five benchmark configs: shapes 1,6,8,11,14), or ids such as 1,3,7 or 1-5,12")
     p.add_argument("--list", action="store_true", help="list the official shapes and exit")
     p.add_argument("--device", default="auto", help="auto, cuda or cuda:0 (one MI355X)")
     p.add_argument("--quick", action="store_true", help="one accuracy trial and fewer timing samples")
@@ -336,7 +336,7 @@ def main(argv: Optional[Sequence[str]] = None) -> int:
     shapes = pkg.OFFICIAL_BENCHMARK_SHAPES
     if args.list:
         for shape_id, config in shapes.items():
-            tag = " (BASELINE config)" if shape_id in pkg.BENCHMARK_CONFIG_SHAPE_IDS else ""
+            tag = " (benchmark config)" if shape_id in pkg.BENCHMARK_CONFIG_SHAPE_IDS else ""
             print(f"shape {shape_id:02d}: {config}{tag}")
         return 0
     try:

@@ -70,7 +70,7 @@ OFFICIAL_BENCHMARK_SHAPES: Dict[int, TransformerConfig] = {
     14: TransformerConfig(32, 100000, 1024, 16, 1024, 2, True),
 }
 
-# The five measured configurations, in BASELINE order, as official shape ids.
+# The five measured configurations, in the benchmark's order (cfg1 to cfg5), as official shape ids.
 BENCHMARK_CONFIG_SHAPE_IDS = (1, 6, 8, 11, 14)
 
 _OFFICIAL_SHAPE_IDS_BY_CONFIG = {
